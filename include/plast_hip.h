@@ -1,0 +1,215 @@
+/*
+ * plast_hip.h — C-ABI of the MI355X (gfx950) backend for plast's elementwise / broadcast /
+ * reduction hot path. Built as plast_amd/libplast_hip.so.
+ *
+ * Drop-in contract:
+ *  - every <op>_hip_forward / <op>_hip_backward has the reference's ForwardKernel / BackwardKernel
+ *    signature (include/core/op.h:5-6) and fills the GPU slots of `Op` (op.h:39-44) where the
+ *    reference binds <op>_cuda_forward / <op>_cuda_backward (src/core/op.c:11-17);
+ *  - tensor metadata (shape, strides, ndim) is host memory and is read by the host side of each
+ *    entry point, then passed to the kernels by value; `data` / `grad->data` are device pointers;
+ *  - forward kernels overwrite the output; backward kernels accumulate (+=) into input->grad and
+ *    skip inputs with requires_grad == false (include/kernels/kernel_macros.h:40, 310-311);
+ *  - reductions rewrite output->shape/ndim/strides like the reference CPU path
+ *    (src/kernels/cpu/reduce_ops.c:80-81);
+ *  - every entry point returns after its GPU work has completed (the reference synchronises after
+ *    every op: src/kernels/cuda/binary_ops.cu:113), unless the caller switched the library to
+ *    asynchronous mode with plast_hip_set_sync(0), in which case work is ordered on the library's
+ *    stream and plast_hip_synchronize() waits for it;
+ *  - errors never cross the ABI as exceptions: a message goes to stderr, as in the reference
+ *    (include/kernels/cuda/cuda_check.h:6-14), and is also kept for plast_hip_last_error().
+ */
+#ifndef PLAST_HIP_H
+#define PLAST_HIP_H
+
+#include "plast_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLAST_HIP_KERNEL_PAIR(name)                                                                \
+  void name##_hip_forward(const Tensor **inputs, Tensor *output, KernelParams params);             \
+  void name##_hip_backward(Tensor **inputs, const Tensor *output, KernelParams params);
+
+/* Binary ops: replace {add,sub,mul,div}_cuda_forward/backward (include/kernels/ops/binary.h:21-24).
+ * inputs[0], inputs[1] broadcast against each other numpy-style (right-aligned, size-1 axes read
+ * coordinate 0: include/kernels/kernel_macros.h:156-168); output has the broadcast shape. */
+PLAST_HIP_KERNEL_PAIR(add)
+PLAST_HIP_KERNEL_PAIR(sub)
+PLAST_HIP_KERNEL_PAIR(mul)
+PLAST_HIP_KERNEL_PAIR(div)
+
+/* Unary ops: replace {abs,cos,sin,tan,exp,log,neg,leaky_relu}_cuda_forward/backward
+ * (include/kernels/ops/unary.h:25-28). leaky_relu's slope is params.fval (unary_ops.c:323). */
+PLAST_HIP_KERNEL_PAIR(exp)
+PLAST_HIP_KERNEL_PAIR(log)
+PLAST_HIP_KERNEL_PAIR(neg)
+PLAST_HIP_KERNEL_PAIR(abs)
+PLAST_HIP_KERNEL_PAIR(sin)
+PLAST_HIP_KERNEL_PAIR(cos)
+PLAST_HIP_KERNEL_PAIR(tan)
+PLAST_HIP_KERNEL_PAIR(leaky_relu)
+
+/* Reductions: replace {sum,mean,max,min}_cuda_forward/backward (include/kernels/ops/reduce.h:21-24).
+ * params.dim = axis, or PLAST_DIM_ALL for all elements; params.keepdim = 0/1. */
+PLAST_HIP_KERNEL_PAIR(sum)
+PLAST_HIP_KERNEL_PAIR(mean)
+PLAST_HIP_KERNEL_PAIR(max)
+PLAST_HIP_KERNEL_PAIR(min)
+
+/* argmax: no reference counterpart (OP_TYPE has none: include/core/op.h:8-37). First index of the
+ * maximum along params.dim (a NaN counts as the maximum), int64 output (dtype INT64); backward is a
+ * no-op. */
+PLAST_HIP_KERNEL_PAIR(argmax)
+
+/* View ops: metadata-only forwards that alias data and rewrite shape/strides on the host, as the
+ * reference's CPU functions do when bound to the GPU slot (src/core/op.c:28-35, ops.def:14-19,24,
+ * src/kernels/cpu/shape_ops.c:28-80); backwards accumulate on the GPU. */
+PLAST_HIP_KERNEL_PAIR(view)
+PLAST_HIP_KERNEL_PAIR(flatten)
+PLAST_HIP_KERNEL_PAIR(squeeze)
+PLAST_HIP_KERNEL_PAIR(unsqueeze)
+PLAST_HIP_KERNEL_PAIR(expand)
+PLAST_HIP_KERNEL_PAIR(broadcast)
+PLAST_HIP_KERNEL_PAIR(transpose)
+
+/* Fused elementwise chain: no reference counterpart (the reference fuses only matmul/conv
+ * epilogues: src/scheduler/fusion.c:28-90). params.dim holds a `const PlastFusedTape *` (host
+ * memory); inputs are the chain's external tensors in tape order. One kernel launch. */
+PLAST_HIP_KERNEL_PAIR(fused_elementwise)
+
+/* Softmax cross-entropy: no reference op; replaces the op chain of src/api/loss.c:97-169 up to NEG.
+ * inputs: [0] logits [N,C] fp32, [1] labels [N] int32, [2] stats [N,2] fp32 (written by forward:
+ * row max and log of the row's exp-sum; read by backward). output: [N] fp32 per-row loss. Backward:
+ * logits->grad += dloss[i] * (softmax - onehot). */
+PLAST_HIP_KERNEL_PAIR(softmax_cross_entropy)
+
+#undef PLAST_HIP_KERNEL_PAIR
+
+/* ------------------------------------------------------------------ fused-chain tape --------- */
+
+/* A fused chain is a straight-line program over one accumulator: the first instruction loads an
+ * external input, every later instruction combines the accumulator with an external input, an
+ * immediate or itself. This covers every chain the fusion pass forms (each fused node consumes the
+ * previous node's output plus at most one external tensor). */
+typedef enum PlastTapeOp {
+  TAPE_LOAD = 0, /* acc = in[src] */
+  TAPE_ADD,
+  TAPE_SUB,
+  TAPE_MUL,
+  TAPE_DIV,      /* binary: acc = acc OP operand, or operand OP acc when acc_rhs */
+  TAPE_LEAKY_RELU, /* acc = acc > 0 ? acc : acc * imm */
+  TAPE_EXP,
+  TAPE_LOG,
+  TAPE_NEG,      /* the reference's neg: 0 - acc inside its 8-wide SIMD blocks, -acc in the tail */
+  TAPE_ABS,
+  TAPE_SIN,
+  TAPE_COS,
+  TAPE_TAN,
+  TAPE_NUM_OPS
+} PlastTapeOp;
+
+typedef enum PlastTapeSrc { TAPE_SRC_NONE = 0, TAPE_SRC_INPUT, TAPE_SRC_ACC, TAPE_SRC_IMM } PlastTapeSrc;
+
+#define PLAST_TAPE_MAX_INS 16
+#define PLAST_TAPE_MAX_INPUTS 4
+
+typedef struct PlastTapeIns {
+  u8 op;      /* PlastTapeOp */
+  u8 src;     /* PlastTapeSrc of the second operand (binary ops) */
+  u8 idx;     /* input index when src == TAPE_SRC_INPUT */
+  u8 acc_rhs; /* 1: operand OP acc (order matters for SUB and DIV) */
+  float imm;  /* leaky slope, or the operand when src == TAPE_SRC_IMM */
+} PlastTapeIns;
+
+typedef struct PlastFusedTape {
+  u32 num_inputs;
+  u32 num_ins;
+  PlastTapeIns ins[PLAST_TAPE_MAX_INS];
+} PlastFusedTape;
+
+/* ------------------------------------------------------------------ op table ----------------- */
+
+/* GPU slots for every OP_TYPE this backend implements (CPU slots left NULL): the table the
+ * reference's get_op_impl builds from include/core/ops.def (src/core/op.c:37-49). Unimplemented
+ * ops (MATMUL, CONV2D and their fused forms) get NULL GPU slots. */
+Op plast_hip_get_op_impl(OP_TYPE op_type);
+
+/* ------------------------------------------------------------------ scheduler pass ----------- */
+
+/* Allocator used by the pass for fused Nodes, input arrays and tapes; pass the reference's
+ * arena_alloc (include/core/arena.h:37) with dag->arena, as fusion_apply does
+ * (src/scheduler/fusion.c:106). */
+typedef void *(*PlastArenaAllocFn)(Arena *arena, u64 size, u64 align);
+
+/* Elementwise-chain fusion over a topologically sorted DAG (the output of build_dag,
+ * src/core/graph.c:52-55): every maximal run of GPU elementwise nodes in which each intermediate
+ * tensor feeds only the next node, nothing in the run requires grad, and the chain has at most
+ * PLAST_TAPE_MAX_INPUTS external inputs is replaced by one FUSED_ELEMENTWISE node writing the last
+ * node's output, spliced into the node array the way fusion_apply does (fusion.c:155-206).
+ * Returns the number of chains fused. Called from fusion_optimize (fusion.c:209-224). */
+u32 plast_hip_fuse_elementwise_chains(DAG *dag, PlastArenaAllocFn alloc);
+
+/* ------------------------------------------------------------------ L0/L1 hooks -------------- */
+
+/* Arena device hooks: replace arena_*_cuda (include/core/arena_cuda.h:9-14), called from
+ * src/core/arena.c:20-24, 83-87, 98-102 and 108-127. Allocation failure prints and exits, as the
+ * reference does (src/core/arena_cuda.cu:5-11). */
+void *arena_alloc_hip(u64 size);
+void arena_free_hip(void *ptr);
+void arena_memset_hip(void *ptr, int value, u64 size);
+void arena_memcpy_h2d_hip(void *dest, const void *src, u64 size);
+void arena_memcpy_d2h_hip(void *dest, const void *src, u64 size);
+void arena_memcpy_d2d_hip(void *dest, const void *src, u64 size);
+
+/* Tensor fill hooks: replace zeros_cuda / ones_cuda / set_ones_grad_cuda
+ * (include/kernels/cuda/cuda_tensor_init.h:9-11), called from src/core/tensor.c:86-89, 105-120,
+ * 147-151. */
+void zeros_hip(Tensor *t, u64 num_elements);
+void ones_hip(Tensor *t, u64 num_elements);
+void set_ones_grad_hip(Tensor *t);
+
+/* Shape-op backward hooks: replace reshape_backward_cuda / transpose_backward_cuda
+ * (src/kernels/cpu/shape_ops.c:7-12). Shape and strides are host arrays. */
+void reshape_backward_hip(float *da, const float *dout, u64 num_elements);
+void transpose_backward_hip(float *da, const float *dout, const u64 *a_shape, const u64 *da_strides,
+                            const u64 *dout_strides, u64 ndim, u64 axis1, u64 axis2,
+                            u64 num_elements);
+
+/* ------------------------------------------------------------------ runtime control ---------- */
+
+/* Select the device (once per process, before any other call; default device 0). Returns 0 on
+ * success. */
+int plast_hip_init(int device);
+/* 1 (default): every entry point waits for its GPU work before returning. 0: asynchronous. */
+void plast_hip_set_sync(int sync);
+/* Wait for all work queued on the library stream. Returns 0 on success. */
+int plast_hip_synchronize(void);
+/* The library's stream (a hipStream_t), for callers that order their own work against it. */
+void *plast_hip_stream(void);
+/* Number of errors since the last plast_hip_clear_error(), and the most recent message. */
+int plast_hip_error_count(void);
+const char *plast_hip_last_error(void);
+void plast_hip_clear_error(void);
+
+/* Device time between two marks recorded on the library stream, in milliseconds. */
+int plast_hip_timer_begin(void);
+float plast_hip_timer_end(void);
+
+/* Deterministic device-side input generation for tests and benchmarks: element i depends only on
+ * (seed, i) (a counter-based hash), so any sub-range can be regenerated independently.
+ * uniform in [lo, hi); normal(mean, std) by Box-Muller; int32 uniform in [lo, hi). */
+void plast_hip_fill_uniform(float *dst, u64 n, u64 seed, float lo, float hi);
+void plast_hip_fill_normal(float *dst, u64 n, u64 seed, float mean, float std);
+void plast_hip_fill_randint(i32 *dst, u64 n, u64 seed, i32 lo, i32 hi);
+
+/* Plain device copy of n floats with the library's streaming load/store path: the measured
+ * bandwidth ceiling the elementwise kernels are compared against. */
+void plast_hip_copy(float *dst, const float *src, u64 n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLAST_HIP_H */

@@ -1,0 +1,108 @@
+// common.hpp — shared host/device machinery of the gfx950 backend: error reporting, the library
+// stream, workspace, 32-bit magic-number division and host-side dimension collapsing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/plast_hip.h"
+
+namespace plast {
+
+constexpr int kMaxRank = PLAST_MAX_NDIM;
+constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 wave64s)
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------- runtime / errors
+
+void report_error(const char *where, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+hipStream_t stream();
+// Called at the end of every entry point: checks the launch and, in synchronous mode, waits.
+void finish(const char *where);
+bool ensure_init();
+// Device scratch of at least `bytes`, owned by the library and reused across calls. Slot 0 holds
+// the reduction engine's partial summaries; slot 1 an op's own temporaries (tie counts, extremes).
+void *workspace(size_t bytes, int slot = 0);
+
+#define PLAST_HIP_TRY(where, expr)                                                                 \
+  do {                                                                                             \
+    hipError_t _e = (expr);                                                                        \
+    if (_e != hipSuccess) {                                                                        \
+      ::plast::report_error(where, "%s: %s", #expr, hipGetErrorString(_e));                        \
+      return;                                                                                      \
+    }                                                                                              \
+  } while (0)
+
+// ------------------------------------------------------------------------- magic division
+
+// Unsigned 32-bit division by a run-time constant d >= 1 using one mul_hi, an add and a shift:
+// q = (umulhi(n, m) + n) >> s, exact for every n < 2^32 (round-up multiplier method,
+// Granlund & Montgomery 1994). The 33-bit intermediate is formed in 64 bits.
+struct MagicDiv {
+  uint32_t mul;
+  uint32_t shift;
+  uint32_t d;
+  static MagicDiv make(uint32_t d) {
+    MagicDiv m;
+    m.d = d;
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    m.shift = s;
+    m.mul = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+    return m;
+  }
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+#ifdef __HIP_DEVICE_COMPILE__
+    uint64_t hi = __umulhi(n, mul);
+#else
+    uint64_t hi = (uint64_t(n) * mul) >> 32;
+#endif
+    return uint32_t((hi + n) >> shift);
+  }
+};
+
+// ------------------------------------------------------------------------- iteration spaces
+
+// An iteration space over `rank` dims (outermost first) shared by up to kMaxOps operands, each with
+// its own element strides (0 on broadcast axes). Built from the reference's Tensor metadata.
+constexpr int kMaxOps = 6;
+
+struct Space {
+  int rank = 0;
+  int nops = 0;
+  uint64_t shape[kMaxRank];
+  int64_t st[kMaxOps][kMaxRank];
+  uint64_t numel() const {
+    uint64_t n = 1;
+    for (int d = 0; d < rank; ++d) n *= shape[d];
+    return n;
+  }
+};
+
+// Right-aligned strides of tensor `t` inside an iteration space of shape `shape[0..rank)`:
+// missing leading axes and size-1 axes get stride 0 (numpy broadcasting, the rule of
+// include/kernels/kernel_macros.h:156-168).
+void bcast_strides(const Tensor *t, const uint64_t *shape, int rank, int64_t *out);
+
+// Drop size-1 axes and merge neighbouring axes that are jointly contiguous for every operand.
+void collapse(Space &s);
+
+// Numpy broadcast shape of two tensors; false when incompatible (cpu_utils.c:78-100).
+bool broadcast_shape(const Tensor *a, const Tensor *b, uint64_t *shape, int *rank);
+
+uint64_t numel(const Tensor *t);
+bool same_shape(const Tensor *a, const Tensor *b);
+// Row-major contiguity with every stride checked (size-1 axes ignored).
+bool contiguous(const Tensor *t);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline unsigned ceil_div(uint64_t a, uint64_t b) { return unsigned((a + b - 1) / b); }
+
+// Reference AVX2 block end: contiguous loops are 8-wide SIMD below n - n%8 (kernel_macros.h:195).
+inline uint64_t simd_end(uint64_t n) { return n - n % 8; }
+
+}  // namespace plast

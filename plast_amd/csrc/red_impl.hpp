@@ -1,0 +1,758 @@
+// red_impl.hpp — the reduction engine.
+//
+// A reduction problem is a Space whose last operand is the target: the target has stride 0 on
+// every reduced axis. After collapsing, one of three kernel families runs:
+//   rows   — the only reduced axis is the innermost and is unit-stride: one wave64 per (row,
+//            segment), float4 loads, wave shuffle reduction; long rows split into segments whose
+//            partials a finalize pass combines in order;
+//   cols   — the innermost axis is kept and unit-stride, one reduced axis: each lane owns four
+//            adjacent outputs and walks its chunk of the reduced axis in order; chunks combine in
+//            order in a finalize pass (no atomics anywhere, so results are deterministic);
+//   generic— any layout: one lane per output, serial walk in index order.
+//
+// Max/min reproduce the reference's literal fold `acc > x ? acc : x` from -FLT_MAX
+// (reduce_ops.c:9, 26-30) bit for bit, including NaN (a NaN resets the fold: the result is the
+// fold of what follows the last NaN) and signed zeros (ties keep the later element). Per index
+// range the fold is summarised as (r, flags): r is the fold started at the range's first element,
+// INDEP set when the range contains a NaN (then the range's result does not depend on what came
+// before). Ranges combine in index order.
+#pragma once
+
+#include <cfloat>
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace plast {
+
+// ------------------------------------------------------------------------- producers
+// A producer turns the NIN operand values at one point of the space into the reduced value.
+
+struct Load1 {
+  static constexpr int NIN = 1;
+  __device__ __forceinline__ float eval(const float *v) const { return v[0]; }
+};
+
+// 1 where a == e (e broadcast from the forward output), else 0: tie count of max/min backward.
+struct EqualCount {
+  static constexpr int NIN = 2;
+  __device__ __forceinline__ float eval(const float *v) const { return v[0] == v[1] ? 1.0f : 0.0f; }
+};
+
+// ------------------------------------------------------------------------- combiners
+
+enum class Post : int { Write = 0, Mean = 1, Accum = 2 };
+
+struct SumComb {
+  using Part = float;
+  using Out = float;
+  static constexpr bool kExact = false;
+  __device__ static Part empty() { return 0.0f; }
+  // the reference's accumulator starts at 0.0f, so a lone -0 sums to +0
+  __device__ static void first(Part &p, float x, int64_t) { p = 0.0f + x; }
+  __device__ static void next(Part &p, float x, int64_t) { p = p + x; }
+  __device__ static Part merge(Part a, Part b) { return a + b; }
+  __device__ static Part shfl(Part p, int m) { return __shfl_xor(p, m); }
+};
+
+// Exact max (IS_MAX) / min fold summaries.
+constexpr uint32_t kIndep = 1, kNonEmpty = 2;
+struct ExtPart {
+  float r;
+  uint32_t flags;
+};
+
+template <bool IS_MAX>
+struct ExtComb {
+  using Part = ExtPart;
+  using Out = float;
+  static constexpr bool kExact = true;
+  __device__ static float pick(float acc, float x) {
+    if constexpr (IS_MAX) return acc > x ? acc : x;
+    else return acc < x ? acc : x;
+  }
+  __device__ static float init() { return IS_MAX ? -FLT_MAX : FLT_MAX; }
+  __device__ static Part empty() { return Part{0.0f, 0u}; }
+  __device__ static void first(Part &p, float x, int64_t) {
+    p.r = x;
+    p.flags = kNonEmpty | (x != x ? kIndep : 0u);
+  }
+  __device__ static void next(Part &p, float x, int64_t) {
+    p.r = pick(p.r, x);
+    if (x != x) p.flags |= kIndep;
+  }
+  // a covers earlier indices than b
+  __device__ static Part merge(Part a, Part b) {
+    if (!(b.flags & kNonEmpty)) return a;
+    if (!(a.flags & kNonEmpty) || (b.flags & kIndep)) return b;
+    return Part{pick(a.r, b.r), a.flags};
+  }
+  // value of the reference's accumulator after folding the whole summarised range from init
+  __device__ static float finish(Part p) {
+    if (!(p.flags & kNonEmpty)) return init();
+    if (p.flags & kIndep) return p.r;
+    return pick(init(), p.r);
+  }
+};
+
+// numpy argmax: first NaN if any, else first index of the maximum.
+struct ArgPart {
+  float v;
+  int64_t i;
+};
+struct ArgmaxComb {
+  using Part = ArgPart;
+  using Out = int64_t;
+  static constexpr bool kExact = false;
+  __device__ static Part empty() { return Part{-__builtin_huge_valf(), INT64_MAX}; }
+  // Order-free: the better of two (value, index) candidates.
+  __device__ static Part merge(Part a, Part b) {
+    const bool an = a.v != a.v, bn = b.v != b.v;
+    if (an || bn) {
+      if (an && bn) return a.i < b.i ? a : b;
+      return an ? a : b;
+    }
+    if (a.v > b.v) return a;
+    if (b.v > a.v) return b;
+    return a.i < b.i ? a : b;
+  }
+  __device__ static void first(Part &p, float x, int64_t k) { p = Part{x, k}; }
+  __device__ static void next(Part &p, float x, int64_t k) { p = merge(p, Part{x, k}); }
+  __device__ static Part shfl(Part p, int m) {
+    Part q;
+    q.v = __shfl_xor(p.v, m);
+    q.i = __shfl_xor(p.i, m);
+    return q;
+  }
+};
+
+// ------------------------------------------------------------------------- arguments
+
+template <int NIN>
+struct RedArgs {
+  const float *in[NIN];
+  void *out;
+  int64_t ost[NIN][kMaxRank];  // operand strides on the kept (output) axes, innermost excluded
+  int64_t tst[kMaxRank];       // target strides on the same axes
+  MagicDiv dv[kMaxRank];       // extents of those axes
+  int nouter;                  // number of such axes
+  int64_t rst[NIN];            // operand strides along the reduced axis
+  int64_t kst[NIN];            // operand strides along the kept innermost axis (cols)
+  int64_t tkst;                // target stride along the kept innermost axis (cols)
+  uint64_t len;                // reduced extent
+  uint64_t rows;               // rows (rows kernel) / outer count (cols kernel)
+  uint64_t inner;              // kept innermost extent (cols kernel)
+  uint32_t segs;               // segments per row / chunks of the reduced axis
+  uint64_t seglen;
+  uint32_t vec_mask;           // bit k: operand k is streamed with float4 loads (else splat)
+  void *part;                  // partial summaries [segs][outputs] when segs > 1
+  int post;                    // Post
+  float divisor;               // Mean
+};
+
+// Outer-axis decode: index -> per-operand base offsets and the target offset.
+template <int NIN>
+__device__ __forceinline__ void decode_outer(const RedArgs<NIN> &A, uint32_t idx, int64_t *base,
+                                             int64_t &tbase) {
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) base[k] = 0;
+  tbase = 0;
+  for (int d = A.nouter - 1; d >= 0; --d) {
+    const uint32_t nxt = A.dv[d].div(idx);
+    const int64_t c = int64_t(idx - nxt * A.dv[d].d);
+    idx = nxt;
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) base[k] += c * A.ost[k][d];
+    tbase += c * A.tst[d];
+  }
+}
+
+template <class Comb>
+__device__ __forceinline__ void store_final(void *out, int64_t off, const typename Comb::Part &p,
+                                            int post, float divisor) {
+  if constexpr (std::is_same<Comb, ArgmaxComb>::value) {
+    static_cast<int64_t *>(out)[off] = p.i == INT64_MAX ? 0 : p.i;
+  } else if constexpr (Comb::kExact) {
+    static_cast<float *>(out)[off] = Comb::finish(p);
+  } else {
+    float *o = static_cast<float *>(out);
+    if (post == int(Post::Accum)) o[off] = o[off] + p;
+    else if (post == int(Post::Mean)) o[off] = p / divisor;
+    else o[off] = p;
+  }
+}
+
+// ------------------------------------------------------------------------- rows kernel
+
+template <class Prod, int NIN>
+__device__ __forceinline__ float value_at(const RedArgs<NIN> &A, const Prod &prod,
+                                          const int64_t *base, uint64_t i) {
+  float v[NIN];
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) v[k] = A.in[k][base[k] + int64_t(i) * A.rst[k]];
+  return prod.eval(v);
+}
+
+template <class T>
+__device__ __forceinline__ T wave_max_t(T v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    T o = __shfl_xor(v, m);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_fmax(float v, bool is_max) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    float o = __shfl_xor(v, m);
+    v = is_max ? fmaxf(v, o) : fminf(v, o);
+  }
+  return v;
+}
+__device__ __forceinline__ bool wave_any(bool b) { return __any(b); }
+
+// Exact fold summary of [b, e) by one wave, used when the fast path saw a NaN or a zero extreme.
+template <bool IS_MAX, class Prod, int NIN>
+__device__ ExtPart exact_range(const RedArgs<NIN> &A, const Prod &prod, const int64_t *base,
+                               uint64_t b, uint64_t e, int lane) {
+  // last NaN
+  int64_t last_nan = -1;
+  for (uint64_t i = b + lane; i < e; i += 64) {
+    const float x = value_at(A, prod, base, i);
+    if (x != x) last_nan = int64_t(i);
+  }
+  last_nan = wave_max_t(last_nan);
+  const uint64_t s = last_nan >= 0 ? uint64_t(last_nan) + 1 : b;
+  if (s >= e) {
+    // the range ends in a NaN: the fold's value is that NaN
+    return ExtPart{value_at(A, prod, base, uint64_t(last_nan)), kNonEmpty | kIndep};
+  }
+  float m = IS_MAX ? -__builtin_huge_valf() : __builtin_huge_valf();
+  for (uint64_t i = s + lane; i < e; i += 64) {
+    const float x = value_at(A, prod, base, i);
+    m = IS_MAX ? fmaxf(m, x) : fminf(m, x);
+  }
+  m = wave_fmax(m, IS_MAX);
+  float r = m;
+  if (m == 0.0f) {
+    // several zeros may tie: the fold keeps the last one, whose sign decides the bits
+    int64_t last_zero = -1;
+    for (uint64_t i = s + lane; i < e; i += 64)
+      if (value_at(A, prod, base, i) == 0.0f) last_zero = int64_t(i);
+    last_zero = wave_max_t(last_zero);
+    r = value_at(A, prod, base, uint64_t(last_zero));
+  }
+  return ExtPart{r, kNonEmpty | (last_nan >= 0 ? kIndep : 0u)};
+}
+
+constexpr int kRowUnroll = 4;  // float4 loads in flight per lane per operand
+
+template <class Prod, class Comb, bool VEC>
+__global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, Prod prod) {
+  constexpr int NIN = Prod::NIN;
+  using Part = typename Comb::Part;
+  const int lane = threadIdx.x & 63;
+  const uint64_t task = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (task >= A.rows * A.segs) return;  // whole wave exits together
+  const uint32_t row = uint32_t(task / A.segs);
+  const uint32_t seg = uint32_t(task - uint64_t(row) * A.segs);
+  int64_t base[NIN], tbase;
+  decode_outer(A, row, base, tbase);
+  const uint64_t b = uint64_t(seg) * A.seglen;
+  const uint64_t e = b + A.seglen < A.len ? b + A.seglen : A.len;
+
+  Part p;
+  if constexpr (Comb::kExact) {
+    // fast path: plain extreme ignoring NaN, plus a NaN flag
+    constexpr bool IS_MAX = std::is_same<Comb, ExtComb<true>>::value;
+    float m = IS_MAX ? -__builtin_huge_valf() : __builtin_huge_valf();
+    bool nan = false;
+    auto take = [&](float x) {
+      m = IS_MAX ? fmaxf(m, x) : fminf(m, x);
+      nan = nan || (x != x);
+    };
+    if constexpr (VEC) {
+      for (uint64_t i0 = b + uint64_t(lane) * 4; i0 < e; i0 += 256 * kRowUnroll) {
+        f4 x[kRowUnroll][NIN];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const uint64_t i = i0 + uint64_t(u) * 256;
+          if (i < e)
+#pragma unroll
+            for (int k = 0; k < NIN; ++k)
+              x[u][k] = (A.vec_mask >> k & 1u)
+                            ? __builtin_nontemporal_load(
+                                  reinterpret_cast<const f4 *>(A.in[k] + base[k] + int64_t(i)))
+                            : f4(A.in[k][base[k]]);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          if (i0 + uint64_t(u) * 256 >= e) continue;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float v[NIN];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = x[u][k][c];
+            take(prod.eval(v));
+          }
+        }
+      }
+    } else {
+      for (uint64_t i = b + lane; i < e; i += 64) take(value_at(A, prod, base, i));
+    }
+    m = wave_fmax(m, IS_MAX);
+    nan = wave_any(nan);
+    if (!nan && m != 0.0f) {
+      p = ExtPart{m, e > b ? kNonEmpty : 0u};
+    } else if (e > b) {
+      p = exact_range<IS_MAX>(A, prod, base, b, e, lane);
+    } else {
+      p = Comb::empty();
+    }
+  } else {
+    p = Comb::empty();
+    Part acc[4] = {Comb::empty(), Comb::empty(), Comb::empty(), Comb::empty()};
+    if constexpr (VEC) {
+      for (uint64_t i0 = b + uint64_t(lane) * 4; i0 < e; i0 += 256 * kRowUnroll) {
+        f4 x[kRowUnroll][NIN];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const uint64_t i = i0 + uint64_t(u) * 256;
+          if (i < e)
+#pragma unroll
+            for (int k = 0; k < NIN; ++k)
+              x[u][k] = (A.vec_mask >> k & 1u)
+                            ? __builtin_nontemporal_load(
+                                  reinterpret_cast<const f4 *>(A.in[k] + base[k] + int64_t(i)))
+                            : f4(A.in[k][base[k]]);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const uint64_t i = i0 + uint64_t(u) * 256;
+          if (i >= e) continue;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float v[NIN];
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) v[k] = x[u][k][c];
+            Comb::next(acc[c], prod.eval(v), int64_t(i + c));
+          }
+        }
+      }
+      p = Comb::merge(Comb::merge(acc[0], acc[1]), Comb::merge(acc[2], acc[3]));
+    } else {
+      for (uint64_t i = b + lane; i < e; i += 64) {
+        Comb::next(p, value_at(A, prod, base, i), int64_t(i));
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) p = Comb::merge(p, Comb::shfl(p, m));
+  }
+
+  if (lane != 0) return;
+  if (A.segs == 1) {
+    store_final<Comb>(A.out, tbase, p, A.post, A.divisor);
+  } else {
+    static_cast<Part *>(A.part)[task] = p;
+  }
+}
+
+// Combine the segments of each row in index order.
+template <class Comb>
+__global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
+  using Part = typename Comb::Part;
+  const uint64_t row = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (row >= A.rows) return;
+  const Part *part = static_cast<const Part *>(A.part) + row * A.segs;
+  Part p = part[0];
+  for (uint32_t s = 1; s < A.segs; ++s) p = Comb::merge(p, part[s]);
+  int64_t base[1], tbase;
+  decode_outer(A, uint32_t(row), base, tbase);
+  store_final<Comb>(A.out, tbase, p, A.post, A.divisor);
+}
+
+// ------------------------------------------------------------------------- cols kernel
+
+constexpr int kColUnroll = 4;
+
+// grid.x: (outer index, block of kBlock lanes along the kept innermost axis); grid.y: chunk.
+template <class Prod, class Comb, bool VEC>
+__global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, Prod prod,
+                                                          uint32_t xblocks) {
+  constexpr int NIN = Prod::NIN;
+  constexpr int W = VEC ? 4 : 1;
+  using Part = typename Comb::Part;
+  const uint32_t o = blockIdx.x / xblocks;
+  const uint64_t j = (uint64_t(blockIdx.x - o * xblocks) * kBlock + threadIdx.x) * W;
+  if (j >= A.inner) return;
+  const uint32_t chunk = blockIdx.y;
+  int64_t base[NIN], tbase;
+  decode_outer(A, o, base, tbase);
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) base[k] += int64_t(j) * A.kst[k];
+  const uint64_t k0 = uint64_t(chunk) * A.seglen;
+  const uint64_t k1 = k0 + A.seglen < A.len ? k0 + A.seglen : A.len;
+
+  Part p[W];
+#pragma unroll
+  for (int c = 0; c < W; ++c) p[c] = Comb::empty();
+  for (uint64_t r0 = k0; r0 < k1; r0 += kColUnroll) {
+    float xv[kColUnroll][NIN][W];
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      const uint64_t r = r0 + u;
+      if (r >= k1) continue;
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) {
+        const float *src = A.in[k] + base[k] + int64_t(r) * A.rst[k];
+        if constexpr (VEC) {
+          const f4 v = (A.vec_mask >> k & 1u) ? *reinterpret_cast<const f4 *>(src) : f4(src[0]);
+#pragma unroll
+          for (int c = 0; c < W; ++c) xv[u][k][c] = v[c];
+        } else {
+          xv[u][k][0] = src[0];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kColUnroll; ++u) {
+      const uint64_t r = r0 + u;
+      if (r >= k1) continue;
+#pragma unroll
+      for (int c = 0; c < W; ++c) {
+        float v[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
+        const float y = prod.eval(v);
+        if (r == k0) Comb::first(p[c], y, int64_t(r));
+        else Comb::next(p[c], y, int64_t(r));
+      }
+    }
+  }
+  const uint64_t nout_inner = A.inner;
+#pragma unroll
+  for (int c = 0; c < W; ++c) {
+    if (A.segs == 1) {
+      store_final<Comb>(A.out, tbase + int64_t(j + c) * A.tkst, p[c], A.post, A.divisor);
+    } else {
+      const uint64_t oi = uint64_t(o) * nout_inner + j + c;
+      static_cast<Part *>(A.part)[uint64_t(chunk) * (A.rows * nout_inner) + oi] = p[c];
+    }
+  }
+}
+
+template <class Comb>
+__global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<1> A) {
+  using Part = typename Comb::Part;
+  const uint64_t oi = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const uint64_t nout = A.rows * A.inner;
+  if (oi >= nout) return;
+  const Part *part = static_cast<const Part *>(A.part);
+  Part p = part[oi];
+  for (uint32_t s = 1; s < A.segs; ++s) p = Comb::merge(p, part[uint64_t(s) * nout + oi]);
+  const uint32_t o = uint32_t(oi / A.inner);
+  const uint64_t j = oi - uint64_t(o) * A.inner;
+  int64_t base[1], tbase;
+  decode_outer(A, o, base, tbase);
+  store_final<Comb>(A.out, tbase + int64_t(j) * A.tkst, p, A.post, A.divisor);
+}
+
+// ------------------------------------------------------------------------- generic kernel
+
+template <int NIN>
+struct GenArgs {
+  const float *in[NIN];
+  void *out;
+  int nk, nr;                      // kept / reduced axis counts
+  uint64_t kext[kMaxRank], rext[kMaxRank];
+  int64_t kst[NIN + 1][kMaxRank];  // strides on kept axes (operand NIN = target)
+  int64_t rst[NIN][kMaxRank];      // strides on reduced axes
+  uint64_t nout, len;
+  int post;
+  float divisor;
+};
+
+template <class Prod, class Comb>
+__global__ __launch_bounds__(kBlock) void red_generic_kernel(GenArgs<Prod::NIN> A, Prod prod) {
+  constexpr int NIN = Prod::NIN;
+  using Part = typename Comb::Part;
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t o = uint64_t(blockIdx.x) * kBlock + threadIdx.x; o < A.nout; o += stride) {
+    int64_t base[NIN] = {};
+    int64_t tbase = 0;
+    uint64_t rem = o;
+    for (int d = A.nk - 1; d >= 0; --d) {
+      const int64_t c = int64_t(rem % A.kext[d]);
+      rem /= A.kext[d];
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) base[k] += c * A.kst[k][d];
+      tbase += c * A.kst[NIN][d];
+    }
+    Part p = Comb::empty();
+    uint64_t rc[kMaxRank] = {};
+    int64_t off[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) off[k] = base[k];
+    for (uint64_t r = 0; r < A.len; ++r) {
+      float v[NIN];
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) v[k] = A.in[k][off[k]];
+      const float y = prod.eval(v);
+      if (r == 0) Comb::first(p, y, int64_t(r));
+      else Comb::next(p, y, int64_t(r));
+      // odometer step over the reduced axes, innermost fastest
+      for (int d = A.nr - 1; d >= 0; --d) {
+        if (++rc[d] < A.rext[d]) {
+#pragma unroll
+          for (int k = 0; k < NIN; ++k) off[k] += A.rst[k][d];
+          break;
+        }
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) off[k] -= int64_t(rc[d] - 1) * A.rst[k][d];
+        rc[d] = 0;
+      }
+    }
+    store_final<Comb>(A.out, tbase, p, A.post, A.divisor);
+  }
+}
+
+// ------------------------------------------------------------------------- host dispatch
+
+// Reduce over every axis where operand NIN (the target) has stride 0 and extent > 1.
+// `post` and `divisor` describe the epilogue; `out` is float* or int64_t* per Comb::Out.
+template <class Prod, class Comb>
+bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space s, Post post,
+                      float divisor, const char *where) {
+  constexpr int NIN = Prod::NIN;
+  using Part = typename Comb::Part;
+  s.nops = NIN + 1;
+  // An empty space: every output holds the fold of nothing (sum 0, mean 0/0, max -FLT_MAX, ...).
+  if (s.numel() == 0) {
+    GenArgs<NIN> G;
+    memset(&G, 0, sizeof G);
+    G.out = out;
+    uint64_t nout = 1;
+    for (int d = 0; d < s.rank; ++d) {
+      if (s.st[NIN][d] == 0 && s.shape[d] != 1) continue;  // reduced axis
+      G.kext[G.nk] = s.shape[d];
+      G.kst[NIN][G.nk] = s.st[NIN][d];
+      ++G.nk;
+      nout *= s.shape[d];
+    }
+    if (nout == 0) return true;
+    G.nout = nout;
+    G.len = 0;
+    G.post = int(post);
+    G.divisor = divisor;
+    red_generic_kernel<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(G, prod);
+    return true;
+  }
+  // collapse() never merges a reduced axis with a kept one: the target's stride is 0 on one and
+  // not on the other.
+  collapse(s);
+  const int r = s.rank;
+  int nred = 0, red_ax = -1;
+  uint64_t nout = 1;
+  for (int d = 0; d < r; ++d) {
+    if (s.st[NIN][d] == 0 && s.shape[d] > 1) {
+      ++nred;
+      red_ax = d;
+    } else {
+      nout *= s.shape[d];
+    }
+  }
+  const bool empty_space = false;
+
+  const bool small_idx = s.numel() < (uint64_t(1) << 32) && nout < (uint64_t(1) << 32);
+
+  // ---- rows: single reduced axis, innermost, unit stride for streamed operands
+  if (!empty_space && small_idx && nred == 1 && red_ax == r - 1) {
+    RedArgs<NIN> A;
+    memset(&A, 0, sizeof A);
+    for (int k = 0; k < NIN; ++k) A.in[k] = static_cast<const float *>(in[k]);
+    A.out = out;
+    A.nouter = r - 1;
+    bool vec = s.shape[r - 1] % 4 == 0;
+    for (int k = 0; k < NIN; ++k) {
+      A.rst[k] = s.st[k][r - 1];
+      if (A.rst[k] == 1 && aligned16(in[k])) A.vec_mask |= 1u << k;
+      else if (A.rst[k] != 0) vec = false;
+      if (A.rst[k] == 1 && !aligned16(in[k])) vec = false;
+    }
+    bool unit = true;
+    for (int k = 0; k < NIN; ++k) unit = unit && (A.rst[k] == 0 || A.rst[k] == 1);
+    if (unit) {
+      for (int d = 0; d < r - 1; ++d) {
+        A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
+        A.tst[d] = s.st[NIN][d];
+        for (int k = 0; k < NIN; ++k) {
+          A.ost[k][d] = s.st[k][d];
+          if ((A.vec_mask >> k & 1u) && s.st[k][d] % 4 != 0) vec = false;
+        }
+      }
+      A.len = s.shape[r - 1];
+      A.rows = nout;
+      // enough waves to cover the machine: split long rows when there are few of them
+      uint32_t segs = 1;
+      const uint64_t want_waves = 4096;
+      if (A.rows < want_waves && A.len >= 8192) {
+        uint64_t sg = (want_waves + A.rows - 1) / A.rows;
+        const uint64_t max_sg = A.len / 4096;
+        if (sg > max_sg) sg = max_sg;
+        if (sg > 65535) sg = 65535;
+        segs = uint32_t(sg < 1 ? 1 : sg);
+      }
+      uint64_t seglen = (A.len + segs - 1) / segs;
+      seglen = (seglen + 255) / 256 * 256;
+      segs = uint32_t((A.len + seglen - 1) / seglen);
+      A.segs = segs;
+      A.seglen = seglen;
+      A.post = int(post);
+      A.divisor = divisor;
+      if (segs > 1) {
+        A.part = workspace(sizeof(Part) * A.rows * segs);
+        if (!A.part) return false;
+      }
+      const uint64_t waves = A.rows * segs;
+      const unsigned grid = ceil_div(waves, kBlock / 64);
+      if (vec) red_rows_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod);
+      else red_rows_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod);
+      if (segs > 1) {
+        RedArgs<1> F;
+        memset(&F, 0, sizeof F);
+        F.out = out;
+        F.nouter = A.nouter;
+        for (int d = 0; d < A.nouter; ++d) {
+          F.dv[d] = A.dv[d];
+          F.tst[d] = A.tst[d];
+        }
+        F.rows = A.rows;
+        F.segs = segs;
+        F.part = A.part;
+        F.post = A.post;
+        F.divisor = divisor;
+        red_rows_finalize<Comb><<<ceil_div(A.rows, kBlock), kBlock, 0, stream()>>>(F);
+      }
+      return true;
+    }
+  }
+
+  // ---- cols: innermost axis kept with unit target stride, exactly one reduced axis
+  if (!empty_space && small_idx && nred == 1 && red_ax != r - 1 && s.st[NIN][r - 1] != 0) {
+    RedArgs<NIN> A;
+    memset(&A, 0, sizeof A);
+    for (int k = 0; k < NIN; ++k) A.in[k] = static_cast<const float *>(in[k]);
+    A.out = out;
+    A.inner = s.shape[r - 1];
+    A.tkst = s.st[NIN][r - 1];
+    A.len = s.shape[red_ax];
+    bool vec = A.inner % 4 == 0 && A.tkst == 1;
+    int no = 0;
+    for (int d = 0; d < r - 1; ++d) {
+      if (d == red_ax) continue;
+      A.dv[no] = MagicDiv::make(uint32_t(s.shape[d]));
+      A.tst[no] = s.st[NIN][d];
+      for (int k = 0; k < NIN; ++k) A.ost[k][no] = s.st[k][d];
+      ++no;
+    }
+    A.nouter = no;
+    for (int k = 0; k < NIN; ++k) {
+      A.rst[k] = s.st[k][red_ax];
+      A.kst[k] = s.st[k][r - 1];
+      if (A.kst[k] == 1 && aligned16(in[k])) A.vec_mask |= 1u << k;
+      else if (A.kst[k] != 0) vec = false;
+      if (A.kst[k] == 1 && !aligned16(in[k])) vec = false;
+      if (A.kst[k] == 1) {
+        if (A.rst[k] % 4 != 0) vec = false;
+        for (int d = 0; d < no; ++d)
+          if (A.ost[k][d] % 4 != 0) vec = false;
+      }
+    }
+    A.rows = nout / A.inner;  // outer count
+    const uint32_t W = vec ? 4 : 1;
+    const uint32_t xblocks = ceil_div(A.inner, uint64_t(kBlock) * W);
+    const uint64_t base_blocks = uint64_t(xblocks) * A.rows;
+    // chunk the reduced axis until the grid has ~2048 workgroups, keeping >= 64 rows per chunk
+    uint64_t chunks = 1;
+    if (base_blocks < 2048 && A.len >= 128) {
+      chunks = (2048 + base_blocks - 1) / base_blocks;
+      const uint64_t max_c = A.len / 64;
+      if (chunks > max_c) chunks = max_c;
+      if (chunks > 65535) chunks = 65535;
+      if (chunks < 1) chunks = 1;
+    }
+    uint64_t seglen = (A.len + chunks - 1) / chunks;
+    chunks = (A.len + seglen - 1) / seglen;
+    A.segs = uint32_t(chunks);
+    A.seglen = seglen;
+    A.post = int(post);
+    A.divisor = divisor;
+    if (base_blocks < (uint64_t(1) << 31)) {
+      if (chunks > 1) {
+        A.part = workspace(sizeof(Part) * nout * chunks);
+        if (!A.part) return false;
+      }
+      const dim3 grid{unsigned(base_blocks), unsigned(chunks), 1u};
+      if (vec) red_cols_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
+      else red_cols_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
+      if (chunks > 1) {
+        RedArgs<1> F;
+        memset(&F, 0, sizeof F);
+        F.out = out;
+        F.nouter = A.nouter;
+        for (int d = 0; d < A.nouter; ++d) {
+          F.dv[d] = A.dv[d];
+          F.tst[d] = A.tst[d];
+        }
+        F.tkst = A.tkst;
+        F.inner = A.inner;
+        F.rows = A.rows;
+        F.segs = A.segs;
+        F.part = A.part;
+        F.post = A.post;
+        F.divisor = divisor;
+        red_cols_finalize<Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(F);
+      }
+      return true;
+    }
+  }
+
+  // ---- generic
+  GenArgs<NIN> G;
+  memset(&G, 0, sizeof G);
+  for (int k = 0; k < NIN; ++k) G.in[k] = static_cast<const float *>(in[k]);
+  G.out = out;
+  G.len = 1;
+  for (int d = 0; d < r; ++d) {
+    const bool red = s.st[NIN][d] == 0 && s.shape[d] > 1;
+    if (red) {
+      G.rext[G.nr] = s.shape[d];
+      for (int k = 0; k < NIN; ++k) G.rst[k][G.nr] = s.st[k][d];
+      G.len *= s.shape[d];
+      ++G.nr;
+    } else {
+      G.kext[G.nk] = s.shape[d];
+      for (int k = 0; k <= NIN; ++k) G.kst[k][G.nk] = s.st[k][d];
+      ++G.nk;
+    }
+  }
+  G.nout = nout;
+  G.post = int(post);
+  G.divisor = divisor;
+  uint64_t blocks = (nout + kBlock - 1) / kBlock;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks == 0) blocks = 1;
+  red_generic_kernel<Prod, Comb><<<unsigned(blocks), kBlock, 0, stream()>>>(G, prod);
+  (void)where;
+  return true;
+}
+
+// Accumulating sum into a broadcast target: target[t] += sum over its broadcast axes of prod.
+template <class Prod>
+bool reduce_accumulate(const Prod &prod, const void *const *in, float *target, Space s,
+                       const char *where) {
+  return launch_reduction<Prod, SumComb>(prod, in, target, s, Post::Accum, 1.0f, where);
+}
+
+}  // namespace plast

@@ -1,0 +1,334 @@
+// softmax_ce.hip — fused softmax cross-entropy over the rows of [N, C] logits with int32 labels.
+//
+// Forward, per row (the reference chain MAX -> SUB -> EXP -> SUM -> LOG -> SUB -> MUL(onehot) ->
+// SUM -> NEG of src/api/loss.c:97-169, one HBM read):
+//   m = the reference's max fold from -FLT_MAX (bit-exact, NaN and signed-zero rules included)
+//   s = sum_j expf(x_j - m)         (parallel sum; the reference sums serially)
+//   l = logf(s)
+//   t = 0 + ((x_label - m) - l), or NaN when any other term 0 * ((x_j - m) - l) is NaN
+//   loss = 0 - t inside the reference's SIMD blocks of its NEG node, -t in its tail
+// stats[row] = (m, l) for the backward.
+// Backward: dx[row, j] (+)= dloss[row] * (expf((x - m) - l) - onehot).
+#include <cfloat>
+
+#include "common.hpp"
+
+namespace plast {
+namespace {
+
+constexpr int kCeBlock = 256;
+constexpr int kCeWaves = kCeBlock / 64;
+
+__device__ __forceinline__ float block_sum(float v, float *lds) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kCeWaves; ++w) r += lds[w];
+  return r;
+}
+
+__device__ __forceinline__ float block_fmax(float v, float *lds) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < kCeWaves; ++w) r = fmaxf(r, lds[w]);
+  return r;
+}
+
+__device__ __forceinline__ bool block_any(bool b, float *lds) {
+  return block_sum(b ? 1.0f : 0.0f, lds) > 0.0f;
+}
+
+// The reference's serial max fold, for rows whose fast-path extreme is ambiguous (NaN or zero).
+__device__ float serial_max_fold(const float *row, uint32_t C) {
+  float acc = -FLT_MAX;
+  for (uint32_t j = 0; j < C; ++j) acc = acc > row[j] ? acc : row[j];
+  return acc;
+}
+
+// Row max with exact reference bits: fast block fmax + NaN flag; thread 0 refolds serially when
+// the fast value could differ (a NaN in the row, or a zero maximum whose sign depends on order).
+__device__ __forceinline__ float row_max_exact(float m, bool nan, const float *row, uint32_t C,
+                                               float *lds) {
+  m = block_fmax(m, lds);
+  nan = block_any(nan, lds);
+  if (nan || m == 0.0f) {
+    __syncthreads();
+    if (threadIdx.x == 0) lds[kCeWaves] = serial_max_fold(row, C);
+    __syncthreads();
+    return lds[kCeWaves];
+  }
+  return m > -FLT_MAX ? m : -FLT_MAX;
+}
+
+// Register-resident forward: each lane keeps NV float4 of the row, so the row is read from HBM once.
+template <int NV>
+__global__ __launch_bounds__(kCeBlock) void ce_fwd_reg_kernel(const float *__restrict__ x,
+                                                              const int32_t *__restrict__ lab,
+                                                              float *__restrict__ stats,
+                                                              float *__restrict__ loss, uint32_t C,
+                                                              uint64_t simd_end) {
+  __shared__ float lds[kCeWaves + 1];
+  const uint64_t row = blockIdx.x;
+  const float *xr = x + row * C;
+  const f4 *x4 = reinterpret_cast<const f4 *>(xr);
+  const uint32_t C4 = C / 4;
+  f4 v[NV];
+  float m = -__builtin_huge_valf();
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
+    if (q < C4) {
+      v[i] = __builtin_nontemporal_load(x4 + q);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        m = fmaxf(m, v[i][c]);
+        nan = nan || v[i][c] != v[i][c];
+      }
+    }
+  }
+  const float mx = row_max_exact(m, nan, xr, C, lds);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
+    if (q < C4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s += expf(v[i][c] - mx);
+    }
+  }
+  s = block_sum(s, lds);
+  const float l = logf(s);
+  const int32_t y = lab[row];
+  bool bad = false;
+  float tl = 0.0f;
+  bool have = false;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
+    if (q < C4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float ls = (v[i][c] - mx) - l;
+        const int32_t j = int32_t(q * 4 + c);
+        if (j == y) {
+          tl = ls;
+          have = true;
+        } else {
+          bad = bad || !(fabsf(ls) <= FLT_MAX);  // 0 * (NaN or inf) is NaN
+        }
+      }
+    }
+  }
+  bad = block_any(bad, lds);
+  if (have) {
+    const float t = bad ? __builtin_nanf("") : 0.0f + tl;
+    loss[row] = row < simd_end ? 0.0f - t : -t;
+    stats[2 * row] = mx;
+    stats[2 * row + 1] = l;
+  }
+  // a label outside [0, C) selects no term: t = +0 (or NaN)
+  if (threadIdx.x == 0 && (y < 0 || uint32_t(y) >= C)) {
+    const float t = bad ? __builtin_nanf("") : 0.0f;
+    loss[row] = row < simd_end ? 0.0f - t : -t;
+    stats[2 * row] = mx;
+    stats[2 * row + 1] = l;
+  }
+}
+
+// Any row length or alignment: three passes over the row (max, exp-sum, terms).
+__global__ __launch_bounds__(kCeBlock) void ce_fwd_generic_kernel(const float *__restrict__ x,
+                                                                  const int32_t *__restrict__ lab,
+                                                                  float *__restrict__ stats,
+                                                                  float *__restrict__ loss,
+                                                                  uint32_t C, uint64_t simd_end) {
+  __shared__ float lds[kCeWaves + 1];
+  const uint64_t row = blockIdx.x;
+  const float *xr = x + row * C;
+  float m = -__builtin_huge_valf();
+  bool nan = false;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) {
+    m = fmaxf(m, xr[j]);
+    nan = nan || xr[j] != xr[j];
+  }
+  const float mx = row_max_exact(m, nan, xr, C, lds);
+  float s = 0.0f;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) s += expf(xr[j] - mx);
+  s = block_sum(s, lds);
+  const float l = logf(s);
+  const int32_t y = lab[row];
+  bool bad = false;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) {
+    const float ls = (xr[j] - mx) - l;
+    if (int32_t(j) != y) bad = bad || !(fabsf(ls) <= FLT_MAX);
+  }
+  bad = block_any(bad, lds);
+  if (threadIdx.x == 0) {
+    float t;
+    if (bad) t = __builtin_nanf("");
+    else if (y >= 0 && uint32_t(y) < C) t = 0.0f + ((xr[y] - mx) - l);
+    else t = 0.0f;
+    loss[row] = row < simd_end ? 0.0f - t : -t;
+    stats[2 * row] = mx;
+    stats[2 * row + 1] = l;
+  }
+}
+
+// Backward: grid (row chunks, rows); each lane handles float4s of one row.
+template <bool VEC, bool OVERWRITE>
+__global__ __launch_bounds__(kCeBlock) void ce_bwd_kernel(const float *__restrict__ x,
+                                                          const int32_t *__restrict__ lab,
+                                                          const float *__restrict__ stats,
+                                                          const float *__restrict__ dloss,
+                                                          float *dx, uint32_t C,
+                                                          uint32_t per_block, uint32_t chunks) {
+  const uint64_t row = blockIdx.x / chunks;
+  const uint32_t chunk = blockIdx.x - uint32_t(row) * chunks;
+  const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
+  const int32_t y = lab[row];
+  const uint32_t j0 = chunk * per_block;
+  const uint32_t j1 = j0 + per_block < C ? j0 + per_block : C;
+  const float *xr = x + row * C;
+  float *dr = dx + row * C;
+  if constexpr (VEC) {
+    for (uint32_t j = j0 + threadIdx.x * 4; j < j1; j += kCeBlock * 4) {
+      const f4 xv = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + j));
+      f4 d;
+      if constexpr (!OVERWRITE) d = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(dr + j));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float sm = expf((xv[c] - m) - l);
+        const float oh = int32_t(j + c) == y ? 1.0f : 0.0f;
+        const float gv = g * (sm - oh);
+        if constexpr (OVERWRITE) d[c] = gv;
+        else d[c] = d[c] + gv;
+      }
+      __builtin_nontemporal_store(d, reinterpret_cast<f4 *>(dr + j));
+    }
+  } else {
+    for (uint32_t j = j0 + threadIdx.x; j < j1; j += kCeBlock) {
+      const float sm = expf((xr[j] - m) - l);
+      const float oh = int32_t(j) == y ? 1.0f : 0.0f;
+      const float gv = g * (sm - oh);
+      dr[j] = OVERWRITE ? gv : dr[j] + gv;
+    }
+  }
+}
+
+bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
+  if (x->dtype != FLOAT32 || x->ndim != 2 || !contiguous(x)) {
+    report_error(where, "logits must be a contiguous fp32 [N, C] tensor");
+    return false;
+  }
+  if (lab->dtype != INT32 || numel(lab) != x->shape[0] || !contiguous(lab)) {
+    report_error(where, "labels must be a contiguous int32 tensor of N elements");
+    return false;
+  }
+  if (st->dtype != FLOAT32 || numel(st) != 2 * x->shape[0] || !contiguous(st)) {
+    report_error(where, "stats must be a contiguous fp32 tensor of 2N elements");
+    return false;
+  }
+  if (x->shape[1] >= (uint64_t(1) << 31)) {
+    report_error(where, "rows longer than 2^31 elements are not supported");
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace plast
+
+using namespace plast;
+
+extern "C" {
+
+void softmax_cross_entropy_hip_forward(const Tensor **inputs, Tensor *output, KernelParams params) {
+  (void)params;
+  const char *where = "softmax_cross_entropy_hip_forward";
+  if (!ensure_init()) return;
+  const Tensor *x = inputs[0], *lab = inputs[1], *st = inputs[2];
+  if (!check_ce(x, lab, st, where)) return;
+  const uint64_t N = x->shape[0];
+  const uint32_t C = uint32_t(x->shape[1]);
+  if (output->dtype != FLOAT32 || numel(output) != N || !contiguous(output)) {
+    report_error(where, "output must be a contiguous fp32 tensor of N elements");
+    return;
+  }
+  if (N == 0) return;
+  if (N > 0x7fffffffull) {
+    report_error(where, "more than 2^31 rows");
+    return;
+  }
+  // The NEG node of the reference chain runs over the [N] (or [N,1]) loss tensor.
+  const uint64_t se = simd_end(N);
+  const float *px = static_cast<const float *>(x->data);
+  const int32_t *pl = static_cast<const int32_t *>(lab->data);
+  float *ps = static_cast<float *>(st->data);
+  float *po = static_cast<float *>(output->data);
+  const bool vec = C % 4 == 0 && aligned16(px) && C > 0;
+  const uint32_t C4 = C / 4;
+  const unsigned grid = unsigned(N);
+  if (vec && C4 <= kCeBlock * 8)
+    ce_fwd_reg_kernel<8><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  else if (vec && C4 <= kCeBlock * 16)
+    ce_fwd_reg_kernel<16><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  else if (vec && C4 <= kCeBlock * 32)
+    ce_fwd_reg_kernel<32><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  else
+    ce_fwd_generic_kernel<<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  finish(where);
+}
+
+// params.keepdim == 1 writes the gradient instead of accumulating it, for callers that own a
+// gradient buffer with no other contribution (saves one HBM read of [N, C]).
+void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, KernelParams params) {
+  const char *where = "softmax_cross_entropy_hip_backward";
+  if (!ensure_init()) return;
+  Tensor *x = inputs[0];
+  const Tensor *lab = inputs[1], *st = inputs[2];
+  if (!x->requires_grad || !x->grad) return;
+  if (!check_ce(x, lab, st, where)) return;
+  if (!output->grad || !contiguous(x->grad)) {
+    report_error(where, "needs the loss gradient and a contiguous logits gradient");
+    return;
+  }
+  const uint64_t N = x->shape[0];
+  const uint32_t C = uint32_t(x->shape[1]);
+  if (N == 0 || C == 0) return;
+
+  const float *px = static_cast<const float *>(x->data);
+  float *pd = static_cast<float *>(x->grad->data);
+  const bool vec = C % 4 == 0 && aligned16(px) && aligned16(pd);
+  // each workgroup covers 8 float4 per lane of one row
+  const uint32_t per_block = kCeBlock * 4 * 8;
+  const uint32_t chunks = ceil_div(C, per_block);
+  if (uint64_t(chunks) * N >= (uint64_t(1) << 31)) {
+    report_error(where, "more than 2^31 workgroups");
+    return;
+  }
+  const unsigned grid = unsigned(uint64_t(chunks) * N);
+  const int32_t *pl = static_cast<const int32_t *>(lab->data);
+  const float *ps = static_cast<const float *>(st->data);
+  const float *pg = static_cast<const float *>(output->grad->data);
+  const bool over = params.keepdim == 1;
+  if (vec && over)
+    ce_bwd_kernel<true, true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+  else if (vec)
+    ce_bwd_kernel<true, false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+  else if (over)
+    ce_bwd_kernel<false, true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+  else
+    ce_bwd_kernel<false, false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+  finish(where);
+}
+
+}  // extern "C"

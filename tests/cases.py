@@ -1,0 +1,315 @@
+"""Backend-agnostic op cases: the same seeded inputs run through the compiled reference, the oracle
+and the HIP library, so each pair can be compared.
+
+Shapes follow the reference's own tests (tests/test_ops.py:5-15: SHAPES (4,), (2,3), (3,2,4) and
+its broadcast pairs; tests/test_edge_cases.py:45-147: broadcasts, chains, transposed views) plus
+SIMD-tail lengths (n % 8 != 0), leading/middle/last axis reductions and special values.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from plast_amd.abi import DIM_ALL, KernelParams
+
+
+@dataclass
+class Arr:
+    shape: tuple
+    dist: str = "normal"        # normal | uniform | pos | special | ties | ints
+    seed: int = 0
+    transpose: tuple | None = None   # (d0, d1): present a transposed view of a base of `shape`
+    requires_grad: bool = False
+
+    def base_array(self) -> np.ndarray:
+        rng = np.random.RandomState(self.seed)
+        n = int(np.prod(self.shape)) if self.shape else 1
+        if self.dist == "normal":
+            a = rng.randn(n).astype(np.float32)
+        elif self.dist == "uniform":
+            a = rng.uniform(-1, 1, n).astype(np.float32)
+        elif self.dist == "pos":
+            a = rng.uniform(0.1, 3.0, n).astype(np.float32)
+        elif self.dist == "ties":
+            a = rng.randint(-2, 3, n).astype(np.float32)
+        elif self.dist == "zeros":
+            a = np.where(rng.rand(n) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+            a[rng.rand(n) < 0.3] = -1.0
+        elif self.dist == "special":
+            a = rng.randn(n).astype(np.float32)
+            pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, -3.4e38,
+                             88.7, -103.9, 1.0], dtype=np.float32)
+            pick = rng.rand(n) < 0.25
+            a[pick] = pool[rng.randint(0, len(pool), pick.sum())]
+        elif self.dist == "labels":
+            a = rng.randint(0, self.shape[-1] if len(self.shape) > 1 else 7, n).astype(np.int32)
+        else:
+            raise ValueError(self.dist)
+        return a.reshape(self.shape)
+
+    @property
+    def view_shape(self) -> tuple:
+        if not self.transpose:
+            return tuple(self.shape)
+        s = list(self.shape)
+        d0, d1 = self.transpose
+        s[d0], s[d1] = s[d1], s[d0]
+        return tuple(s)
+
+
+@dataclass
+class Case:
+    id: str
+    op: str
+    kind: str                    # fwd | bwd
+    inputs: list
+    out_shape: tuple
+    params: tuple = (0, 0, 0.0)  # (dim, keepdim, fval)
+    out_dtype: str = "f32"
+    exact: bool = True           # bit-exact expected between oracle and reference
+    dout_seed: int = 99
+    tags: set = field(default_factory=set)
+
+    def kparams(self) -> KernelParams:
+        d, k, f = self.params
+        return KernelParams(d, k, f)
+
+
+def _bshape(a, b):
+    return tuple(np.broadcast_shapes(a, b))
+
+
+def _red_shape(shape, dim, keep):
+    if dim == DIM_ALL:
+        return (1,)
+    s = list(shape)
+    if keep:
+        s[dim] = 1
+    else:
+        s.pop(dim)
+        if not s:
+            s = [1]
+    return tuple(s)
+
+
+BINARY = ["add", "sub", "mul", "div"]
+UNARY = ["exp", "log", "neg", "abs", "sin", "cos", "tan", "leaky_relu"]
+REDUCE = ["sum", "mean", "max", "min"]
+
+SAME_SHAPES = [(4,), (2, 3), (3, 2, 4), (37,), (5, 13), (2, 3, 5, 7)]
+BCAST_PAIRS = [((2, 3), (3,)), ((3, 1), (1, 4)), ((2, 3, 4), (3, 1)), ((4, 3), (1,)),
+               ((2, 1, 5), (3, 1)), ((16, 12), (12,)), ((1, 6), (5, 1))]
+
+
+def build_cases() -> list[Case]:
+    cases: list[Case] = []
+    seed = [1000]
+
+    def s():
+        seed[0] += 1
+        return seed[0]
+
+    # ---- binary forward
+    for op in BINARY:
+        dist_b = "pos" if op == "div" else "normal"
+        for sh in SAME_SHAPES:
+            cases.append(Case(f"{op}_fwd_{sh}", op, "fwd", [Arr(sh, "normal", s()), Arr(sh, dist_b, s())], sh))
+        for sa, sb in BCAST_PAIRS:
+            cases.append(Case(f"{op}_fwd_bc_{sa}_{sb}", op, "fwd",
+                              [Arr(sa, "normal", s()), Arr(sb, dist_b, s())], _bshape(sa, sb)))
+        cases.append(Case(f"{op}_fwd_special", op, "fwd",
+                          [Arr((9, 11), "special", s()), Arr((9, 11), "special", s())], (9, 11)))
+        # a transposed view combined with a broadcast operand (config 3's layout, small)
+        cases.append(Case(f"{op}_fwd_transposed", op, "fwd",
+                          [Arr((3, 6, 5), "normal", s(), transpose=(1, 2)), Arr((5, 1), dist_b, s())],
+                          (3, 5, 6)))
+
+    # ---- unary forward
+    for op in UNARY:
+        dist = "pos" if op == "log" else "normal"
+        alphas = [0.0, 0.01] if op == "leaky_relu" else [0.0]
+        for al in alphas:
+            for sh in [(37,), (2, 3), (3, 2, 4), (64,)]:
+                cases.append(Case(f"{op}{al}_fwd_{sh}", op, "fwd", [Arr(sh, dist, s())], sh, (0, 0, al)))
+            cases.append(Case(f"{op}{al}_fwd_transposed", op, "fwd",
+                              [Arr((4, 7), dist, s(), transpose=(0, 1))], (7, 4), (0, 0, al)))
+            cases.append(Case(f"{op}{al}_fwd_special", op, "fwd", [Arr((53,), "special", s())],
+                              (53,), (0, 0, al)))
+
+    # ---- reductions forward
+    for op in REDUCE + ["argmax"]:
+        odt = "i64" if op == "argmax" else "f32"
+        for sh in [(4,), (2, 3), (3, 2, 4), (5, 130)]:
+            for keep in (0, 1):
+                for dim in list(range(len(sh))) + [DIM_ALL]:
+                    if dim == DIM_ALL and keep:
+                        continue
+                    cases.append(Case(f"{op}_fwd_{sh}_d{dim}_k{keep}", op, "fwd",
+                                      [Arr(sh, "normal", s())], _red_shape(sh, dim, keep),
+                                      (dim, keep, 0.0), odt))
+        for dist in ("special", "ties", "zeros"):
+            for dim in (0, 1, DIM_ALL):
+                cases.append(Case(f"{op}_fwd_{dist}_d{dim}", op, "fwd", [Arr((6, 9), dist, s())],
+                                  _red_shape((6, 9), dim, 0), (dim, 0, 0.0), odt))
+        cases.append(Case(f"{op}_fwd_transposed_d1", op, "fwd",
+                          [Arr((5, 6), "normal", s(), transpose=(0, 1))], (6,), (1, 0, 0.0), odt))
+        cases.append(Case(f"{op}_fwd_transposed_all", op, "fwd",
+                          [Arr((5, 6), "normal", s(), transpose=(0, 1))], (1,), (DIM_ALL, 0, 0.0), odt))
+
+    # ---- binary backward
+    for op in BINARY:
+        dist_b = "pos" if op == "div" else "normal"
+        for sh in [(4,), (37,), (2, 3), (3, 2, 4)]:
+            cases.append(Case(f"{op}_bwd_{sh}", op, "bwd",
+                              [Arr(sh, "normal", s(), requires_grad=True),
+                               Arr(sh, dist_b, s(), requires_grad=True)], sh))
+        for sa, sb in BCAST_PAIRS[:5]:
+            # the reference accumulates broadcast grads with `omp atomic`: order unspecified
+            cases.append(Case(f"{op}_bwd_bc_{sa}_{sb}", op, "bwd",
+                              [Arr(sa, "normal", s(), requires_grad=True),
+                               Arr(sb, dist_b, s(), requires_grad=True)], _bshape(sa, sb),
+                              exact=False))
+        cases.append(Case(f"{op}_bwd_only_b", op, "bwd",
+                          [Arr((3, 5), "normal", s()), Arr((3, 5), dist_b, s(), requires_grad=True)], (3, 5)))
+
+    # ---- unary backward
+    for op in UNARY:
+        dist = "pos" if op == "log" else "normal"
+        alphas = [0.0, 0.01] if op == "leaky_relu" else [0.0]
+        for al in alphas:
+            for sh in [(37,), (3, 2, 4)]:
+                cases.append(Case(f"{op}{al}_bwd_{sh}", op, "bwd", [Arr(sh, dist, s(), requires_grad=True)],
+                                  sh, (0, 0, al)))
+            cases.append(Case(f"{op}{al}_bwd_transposed", op, "bwd",
+                              [Arr((4, 7), dist, s(), transpose=(0, 1), requires_grad=True)],
+                              (7, 4), (0, 0, al)))
+
+    # ---- reduction backward
+    for op in REDUCE:
+        for sh in [(4,), (2, 3), (3, 2, 4)]:
+            for keep in (0, 1):
+                for dim in list(range(len(sh))) + [DIM_ALL]:
+                    if dim == DIM_ALL and keep:
+                        continue
+                    cases.append(Case(f"{op}_bwd_{sh}_d{dim}_k{keep}", op, "bwd",
+                                      [Arr(sh, "normal", s(), requires_grad=True)],
+                                      _red_shape(sh, dim, keep), (dim, keep, 0.0)))
+        if op in ("max", "min"):
+            for dim in (0, 1, DIM_ALL):
+                cases.append(Case(f"{op}_bwd_ties_d{dim}", op, "bwd",
+                                  [Arr((6, 9), "ties", s(), requires_grad=True)],
+                                  _red_shape((6, 9), dim, 0), (dim, 0, 0.0)))
+
+    # ---- transpose backward
+    for sh, ax in [((3, 4), (0, 1)), ((2, 3, 4), (0, 2)), ((2, 3, 4), (1, 2))]:
+        out = list(sh)
+        out[ax[0]], out[ax[1]] = out[ax[1]], out[ax[0]]
+        cases.append(Case(f"transpose_bwd_{sh}_{ax}", "transpose", "bwd",
+                          [Arr(sh, "normal", s(), requires_grad=True)], tuple(out), (ax[0], ax[1], 0.0)))
+    return cases
+
+
+CASES = build_cases()
+
+
+# ------------------------------------------------------------------------------- running
+class Backend:
+    """Adapter: tensor construction and op calls for one implementation."""
+
+    def tensor(self, arr: np.ndarray, requires_grad: bool):
+        raise NotImplementedError
+
+    def view(self, base, shape, strides):
+        raise NotImplementedError
+
+    def empty(self, shape, dtype: str, requires_grad: bool = False):
+        raise NotImplementedError
+
+    def fwd(self, op, ins, out, p):
+        raise NotImplementedError
+
+    def bwd(self, op, ins, out, p):
+        raise NotImplementedError
+
+    def read(self, t) -> np.ndarray:
+        raise NotImplementedError
+
+    def read_grad(self, t) -> np.ndarray:
+        raise NotImplementedError
+
+    def set_grad(self, t, arr: np.ndarray):
+        raise NotImplementedError
+
+
+def materialize(be: Backend, a: Arr):
+    base_arr = a.base_array()
+    if not a.transpose:
+        return be.tensor(base_arr, a.requires_grad), base_arr
+    base = be.tensor(base_arr, a.requires_grad)
+    d0, d1 = a.transpose
+    st = list(np.array(base_arr.strides) // base_arr.itemsize)
+    st[d0], st[d1] = st[d1], st[d0]
+    v = be.view(base, a.view_shape, st)
+    return v, base_arr
+
+
+def run_case(be: Backend, c: Case) -> dict:
+    res = {}
+    ins = [materialize(be, a)[0] for a in c.inputs]
+    p = c.kparams()
+    if c.op == "transpose":
+        # forward is metadata-only; the interesting part is the backward accumulate
+        out = be.empty(c.out_shape, "f32", requires_grad=True)
+        be.fwd("transpose", ins, out, p)
+        g = np.random.RandomState(c.dout_seed).randn(*c.out_shape).astype(np.float32)
+        be.set_grad(out, g)
+        be.bwd("transpose", ins, out, p)
+        res["grad0"] = be.read_grad(ins[0])
+        return res
+    out = be.empty(c.out_shape, c.out_dtype, requires_grad=(c.kind == "bwd"))
+    be.fwd(c.op, ins, out, p)
+    res["out"] = be.read(out)
+    if c.kind == "bwd":
+        g = np.random.RandomState(c.dout_seed).randn(*res["out"].shape).astype(np.float32)
+        be.set_grad(out, g)
+        be.bwd(c.op, ins, out, p)
+        for k, a in enumerate(c.inputs):
+            if a.requires_grad:
+                res[f"grad{k}"] = be.read_grad(ins[k])
+    return res
+
+
+def bits_equal(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """Elementwise bit equality, any NaN matching any NaN (NaN payload and sign are not compared)."""
+    x = np.asarray(x)
+    y = np.asarray(y)
+    if x.dtype != np.float32:
+        return x == y
+    xn, yn = np.isnan(x), np.isnan(y)
+    return (x.view(np.uint32) == y.view(np.uint32)) | (xn & yn)
+
+
+def assert_bits(x, y, what=""):
+    x = np.asarray(x)
+    y = np.asarray(y)
+    assert x.shape == y.shape, f"{what}: shape {x.shape} != {y.shape}"
+    eq = bits_equal(x, y)
+    if not eq.all():
+        i = np.argwhere(~eq)[0]
+        raise AssertionError(f"{what}: {int((~eq).sum())} of {eq.size} differ; first at {tuple(i)}: "
+                             f"{x[tuple(i)]!r} vs {y[tuple(i)]!r}")
+
+
+def assert_close_sum(x, y, scale, rel=1e-5, what=""):
+    """|x - y| <= rel * scale (scale: the sum of |terms| behind each element, or 1 at least)."""
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    assert x.shape == y.shape, f"{what}: shape {x.shape} != {y.shape}"
+    both_nan = np.isnan(x) & np.isnan(y)
+    same_inf = np.isinf(x) & (x == y)
+    ok = both_nan | same_inf | (np.abs(x - y) <= rel * np.maximum(np.asarray(scale, np.float64), 1e-30))
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} out of tolerance; first at "
+                             f"{tuple(i)}: {x[tuple(i)]!r} vs {y[tuple(i)]!r} (scale {np.asarray(scale)[tuple(i)] if np.ndim(scale) else scale})")

@@ -1,0 +1,163 @@
+"""CPU tests that pin the oracle (oracle/oracle.c) before it is trusted as the GPU parity checker:
+against the compiled reference, the committed golden vectors made from it, and closed forms."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from cases import CASES, assert_bits, assert_close_sum, materialize, run_case
+from hostlib import (HostBackend, HostTensor, libm_expf, oracle_backward, oracle_forward,
+                     ref_available, ref_ce_chain)
+from plast_amd.abi import DIM_ALL, KernelParams
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_cases.npz"
+REF_CASES = [c for c in CASES if c.op != "argmax"]
+
+
+def _key(case_id):
+    return re.sub(r"[^A-Za-z0-9_.-]+", "_", case_id)
+
+
+def _compare(c, got: dict, want: dict, what: str):
+    assert set(got) == set(want), f"{c.id}: outputs {sorted(got)} vs {sorted(want)}"
+    for k in want:
+        if c.exact:
+            assert_bits(got[k], want[k], f"{c.id}:{k} ({what})")
+        else:
+            scale = np.abs(want[k]).astype(np.float64) + 1.0
+            assert_close_sum(got[k], want[k], scale, 1e-5, f"{c.id}:{k} ({what})")
+
+
+@pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("c", REF_CASES, ids=[c.id for c in REF_CASES])
+def test_oracle_matches_compiled_reference(c):
+    _compare(c, run_case(HostBackend("oracle"), c), run_case(HostBackend("ref"), c), "vs reference")
+
+
+def test_oracle_matches_golden_vectors():
+    assert GOLDEN.exists(), "tests/golden/reference_cases.npz missing"
+    g = np.load(GOLDEN, allow_pickle=False)
+    checked = 0
+    for c in REF_CASES:
+        k = _key(c.id)
+        for i, a in enumerate(c.inputs):
+            np.testing.assert_array_equal(a.base_array(), g[f"{k}@in{i}"], err_msg=f"{c.id} input {i}")
+        want = {n.split("@", 1)[1]: g[n] for n in g.files
+                if n.startswith(k + "@") and not n[len(k) + 1:].startswith("in")}
+        _compare(c, run_case(HostBackend("oracle"), c), want, "vs golden")
+        checked += 1
+    assert checked == len(REF_CASES)
+
+
+@pytest.mark.parametrize("c", [c for c in CASES if c.op == "argmax"], ids=lambda c: c.id)
+def test_argmax_is_numpy_argmax(c):
+    """argmax has no reference op: it is pinned to numpy.argmax (first max, first NaN)."""
+    out = run_case(HostBackend("oracle"), c)["out"]
+    x = materialize(HostBackend("oracle"), c.inputs[0])[0].numpy()
+    dim, keep, _ = c.params
+    if dim == DIM_ALL:
+        want = np.array([np.argmax(x)])
+    else:
+        want = np.argmax(x, axis=dim)
+        if keep:
+            want = np.expand_dims(want, dim)
+        if want.ndim == 0:
+            want = want.reshape(1)
+    np.testing.assert_array_equal(out, want.astype(np.int64))
+
+
+@pytest.mark.parametrize("n", [1, 7, 1000, 100_003])
+def test_sum_and_mean_within_serial_bound(n):
+    """Serial fp32 summation error is at most (n-1)*u*sum|x| (u = 2^-24): check against fp64."""
+    x = np.random.RandomState(n).randn(n).astype(np.float32)
+    a = HostTensor(x)
+    o = HostTensor(np.zeros(1, np.float32))
+    oracle_forward("sum", [a], o, KernelParams(DIM_ALL, 0, 0.0))
+    s64 = x.astype(np.float64).sum()
+    bound = max(n - 1, 1) * 2.0 ** -24 * np.abs(x).astype(np.float64).sum()
+    assert abs(float(o.numpy()[0]) - s64) <= bound
+    oracle_forward("mean", [a], o, KernelParams(DIM_ALL, 0, 0.0))
+    assert abs(float(o.numpy()[0]) - s64 / n) <= bound / n + 2.0 ** -24 * abs(s64 / n)
+
+
+def test_max_fold_rules():
+    """The literal fold `acc > x ? acc : x` from -FLT_MAX: a NaN resets it, ties keep the later
+    element, all -inf gives -FLT_MAX (reduce_ops.c:9, 26-30)."""
+    def mx(v):
+        a = HostTensor(np.array(v, np.float32))
+        o = HostTensor(np.zeros(1, np.float32))
+        oracle_forward("max", [a], o, KernelParams(DIM_ALL, 0, 0.0))
+        return o.numpy()[0]
+    nan = np.float32("nan")
+    assert np.isnan(mx([1.0, 5.0, nan]))
+    assert mx([1.0, nan, 0.5, -2.0]) == np.float32(0.5)
+    assert mx([-np.inf, -np.inf]) == np.float32(-3.4028235e38)
+    assert np.signbit(mx([0.0, -0.0])) and not np.signbit(mx([-0.0, 0.0]))
+
+
+def test_exp_log_call_glibc():
+    x = np.concatenate([np.random.RandomState(3).uniform(-90, 90, 2000),
+                        [0.0, -0.0, 88.72, -103.97, 1e-40, np.inf, -np.inf, np.nan]]).astype(np.float32)
+    a = HostTensor(x)
+    o = HostTensor(np.zeros_like(x))
+    oracle_forward("exp", [a], o)
+    assert_bits(o.numpy(), libm_expf(x), "exp vs glibc expf")
+
+
+@pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("N,Cn", [(1, 1), (9, 5), (37, 50), (16, 1003)])
+def test_softmax_ce_matches_reference_chain(N, Cn):
+    rng = np.random.RandomState(N * 131 + Cn)
+    x = (rng.randn(N, Cn) * 2).astype(np.float32)
+    lab = rng.randint(0, Cn, N).astype(np.int32)
+    loss_r, mx_r, ls_r, _, dx_r = ref_ce_chain(x, lab)
+    X = HostTensor(x, requires_grad=True)
+    L = HostTensor(lab)
+    S = HostTensor(np.zeros((N, 2), np.float32))
+    O = HostTensor(np.zeros(N, np.float32), requires_grad=True)
+    oracle_forward("softmax_cross_entropy", [X, L, S], O)
+    assert_bits(O.numpy(), loss_r, "row loss")
+    assert_bits(S.numpy()[:, 0], mx_r, "row max")
+    assert_bits(S.numpy()[:, 1], ls_r, "row log-sum")
+    O.grad.buf[:] = np.float32(1.0) / np.float32(N)   # the MEAN node's backward
+    oracle_backward("softmax_cross_entropy", [X, L, S], O)
+    d = X.grad.numpy()
+    # the chain's max path adds only rounding residue; elementwise error ~ a few ulp of 1/N
+    assert np.abs(d - dx_r).max() <= 1e-5 * max(np.abs(dx_r).max(), 1.0 / N)
+
+
+def test_softmax_ce_invariants():
+    rng = np.random.RandomState(11)
+    N, Cn = 64, 300
+    x = (rng.randn(N, Cn) * 2).astype(np.float32)
+    lab = rng.randint(0, Cn, N).astype(np.int32)
+    X = HostTensor(x, requires_grad=True)
+    L = HostTensor(lab)
+    S = HostTensor(np.zeros((N, 2), np.float32))
+    O = HostTensor(np.zeros(N, np.float32), requires_grad=True)
+    oracle_forward("softmax_cross_entropy", [X, L, S], O)
+    st = S.numpy()
+    p = np.exp((x.astype(np.float64) - st[:, :1]) - st[:, 1:])
+    np.testing.assert_allclose(p.sum(1), 1.0, rtol=1e-5)
+    lse = np.log(np.exp(x.astype(np.float64)).sum(1))
+    np.testing.assert_allclose(O.numpy(), lse - x[np.arange(N), lab], rtol=1e-5, atol=1e-5)
+    O.grad.buf[:] = 1.0
+    oracle_backward("softmax_cross_entropy", [X, L, S], O)
+    np.testing.assert_allclose(X.grad.numpy().sum(1), 0.0, atol=1e-5)
+
+
+def test_planted_mistake_is_caught():
+    """The comparison machinery must flag a wrong oracle: plant `add` where `sub` is expected."""
+    c = next(c for c in CASES if c.id.startswith("sub_fwd_(2, 3)"))
+    good = run_case(HostBackend("oracle"), c)
+
+    class Planted(HostBackend):
+        def fwd(self, op, ins, out, p):
+            super().fwd("add" if op == "sub" else op, ins, out, p)
+
+    bad = run_case(Planted("oracle"), c)
+    with pytest.raises(AssertionError):
+        assert_bits(bad["out"], good["out"], "planted")
