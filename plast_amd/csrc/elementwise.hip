@@ -425,11 +425,24 @@ void fused_elementwise_hip_forward(const Tensor **inputs, Tensor *output, Kernel
   // takes its contiguous path whenever the chain's output is contiguous.
   const uint64_t se = contiguous(output) ? simd_end(n) : 0;
   (void)all_contig;
-  switch (nin) {
-  case 1: { TapeBody<1> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-  case 2: { TapeBody<2> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-  case 3: { TapeBody<3> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-  default: { TapeBody<4> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+  bool trig = false;
+  for (uint32_t i = 0; i < tape->num_ins; ++i)
+    trig = trig || tape->ins[i].op == TAPE_SIN || tape->ins[i].op == TAPE_COS ||
+           tape->ins[i].op == TAPE_TAN;
+  if (trig) {
+    switch (nin) {
+    case 1: { TapeBody<1, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    case 2: { TapeBody<2, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    case 3: { TapeBody<3, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    default: { TapeBody<4, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    }
+  } else {
+    switch (nin) {
+    case 1: { TapeBody<1, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    case 2: { TapeBody<2, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    case 3: { TapeBody<3, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    default: { TapeBody<4, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
+    }
   }
   finish(where);
 }

@@ -78,6 +78,14 @@ __device__ __forceinline__ float grad_b(float g, float x, float y, bool simd) {
 
 template <class Derived>
 struct ScalarBody {
+  static constexpr int kUnroll = 4;  // float4 units per lane
+  template <int U, int N>
+  __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
+                                             const bool (&valid)[U], f4 (&acc)[U]) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (valid[u]) acc[u] = eval4(x[u], idx[u]);
+  }
   __device__ __forceinline__ f4 eval4(const f4 *x, uint64_t idx) const {
     const Derived &d = static_cast<const Derived &>(*this);
     constexpr int N = Derived::NIN;
@@ -156,69 +164,161 @@ struct AccumDivBody : ScalarBody<AccumDivBody> {
   }
 };
 
-// Runtime tape interpreter for fused chains. Every branch is on a wave-uniform kernel argument,
-// so the interpretation costs scalar instructions only; the vector work is the chain's own math.
-template <int N>
+// Runtime tape interpreter for fused chains. Every field read is a scalar load of the kernel
+// argument and every branch is on an SGPR value, so the interpretation costs scalar instructions
+// only. The tape loop is the outer loop, so each dispatch is paid once per U float4 units.
+// TRIG: whether sin/cos/tan are compiled in. Their argument reduction needs many registers, so
+// tapes without them run an instantiation that leaves those cases out (and keeps more waves
+// resident).
+template <int N, bool TRIG>
 struct TapeBody {
   static constexpr int NIN = N;
+  static constexpr int kUnroll = 2;  // float4 units per lane: keeps the interpreter under 64 VGPRs
   PlastFusedTape t;
   uint64_t simd_end;
 
-  __device__ __forceinline__ static f4 pick(const f4 *x, int k) {
-    switch (k) {
-    case 0: return x[0];
-    case 1: return x[N > 1 ? 1 : 0];
-    case 2: return x[N > 2 ? 2 : 0];
-    default: return x[N > 3 ? 3 : 0];
-    }
-  }
   template <class F>
   __device__ __forceinline__ static f4 map(f4 a, F f) {
     return f4{f(a[0]), f(a[1]), f(a[2]), f(a[3])};
   }
 
-  __device__ __forceinline__ f4 eval4(const f4 *x, uint64_t idx) const {
-    f4 acc = pick(x, t.ins[0].idx);
-    const bool simd = idx < simd_end;  // idx is a multiple of 4 and simd_end of 8
+  // acc[u] = tape(x[u]); idx[u] is the linear index of unit u's first element (a multiple of 4,
+  // while simd_end is a multiple of 8, so a unit never straddles the NEG rule's boundary).
+  // Invalid units compute on whatever their registers hold; only their stores are skipped.
+  template <int U>
+  __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
+                                             const bool (&valid)[U], f4 (&acc)[U]) const {
+    (void)valid;
+    uint2 w0;
+    __builtin_memcpy(&w0, &t.ins[0], sizeof w0);
+    select_input(x, int((w0.x >> 16) & 0xffu), acc);
+    // not unrolled: the loop sits outside any lane-divergent branch, so i stays uniform and
+    // every t.ins[i] field is an SGPR-offset scalar load
     for (uint32_t i = 1; i < t.num_ins; ++i) {
-      const PlastTapeIns in = t.ins[i];
-      f4 o = acc;
-      if (in.src == TAPE_SRC_INPUT) o = pick(x, in.idx);
-      else if (in.src == TAPE_SRC_IMM) o = f4(in.imm);
-      const f4 l = in.acc_rhs ? o : acc;
-      const f4 r = in.acc_rhs ? acc : o;
-      switch (in.op) {
-      case TAPE_ADD: acc = l + r; break;
-      case TAPE_SUB: acc = l - r; break;
-      case TAPE_MUL: acc = l * r; break;
-      case TAPE_DIV: acc = l / r; break;
-      case TAPE_LEAKY_RELU: {
-        const float al = in.imm;
-        acc = map(acc, [al](float v) { return v > 0.0f ? v : v * al; });
-        break;
+      // one 8-byte scalar load per instruction (scalar loads are dword-granular)
+      uint2 w;
+      __builtin_memcpy(&w, &t.ins[i], sizeof w);
+      const int op = int(w.x & 0xffu), src = int((w.x >> 8) & 0xffu), k = int((w.x >> 16) & 0xffu);
+      const bool rhs = (w.x >> 24) != 0u;
+      const float imm = __uint_as_float(w.y);
+      f4 o[U];
+      if (src == TAPE_SRC_INPUT) {
+        select_input(x, k, o);
+      } else if (src == TAPE_SRC_IMM) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) o[u] = f4(imm);
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) o[u] = acc[u];
       }
-      case TAPE_EXP: acc = map(acc, [](float v) { return expf(v); }); break;
-      case TAPE_LOG: acc = map(acc, [](float v) { return logf(v); }); break;
-      case TAPE_NEG:
-        acc = simd ? f4(0.0f) - acc : map(acc, [](float v) { return -v; });
+      switch (op) {
+      case TAPE_ADD:
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = acc[u] + o[u];  // commutative
         break;
-      case TAPE_ABS: acc = map(acc, [](float v) { return fabsf(v); }); break;
-      case TAPE_SIN: acc = map(acc, [](float v) { return sinf(v); }); break;
-      case TAPE_COS: acc = map(acc, [](float v) { return cosf(v); }); break;
-      case TAPE_TAN: acc = map(acc, [](float v) { return tanf(v); }); break;
-      default: break;
+      case TAPE_MUL:
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = acc[u] * o[u];  // commutative
+        break;
+      case TAPE_SUB:
+        if (rhs) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = o[u] - acc[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = acc[u] - o[u];
+        }
+        break;
+      case TAPE_DIV:
+        if (rhs) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = o[u] / acc[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = acc[u] / o[u];
+        }
+        break;
+      case TAPE_LEAKY_RELU:
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          acc[u] = map(acc[u], [imm](float v) { return v > 0.0f ? v : v * imm; });
+        break;
+      case TAPE_EXP:
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return expf(v); });
+        break;
+      case TAPE_LOG:
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return logf(v); });
+        break;
+      case TAPE_NEG:
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          acc[u] = idx[u] < simd_end ? f4(0.0f) - acc[u] : map(acc[u], [](float v) { return -v; });
+        break;
+      case TAPE_ABS:
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return fabsf(v); });
+        break;
+      case TAPE_SIN:
+        if constexpr (TRIG) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return sinf(v); });
+        }
+        break;
+      case TAPE_COS:
+        if constexpr (TRIG) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return cosf(v); });
+        }
+        break;
+      case TAPE_TAN:
+        if constexpr (TRIG) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return tanf(v); });
+        }
+        break;
+      default:
+        break;
       }
     }
-    return acc;
   }
-  __device__ __forceinline__ float eval(const float *v, uint64_t idx) const {
-    f4 x[N];
+
+  // dst[u] = x[u][k] for a uniform k, one branch for all units
+  template <int U>
+  __device__ __forceinline__ static void select_input(const f4 (&x)[U][N], int k, f4 (&dst)[U]) {
+    switch (k) {
+    case 0:
 #pragma unroll
-    for (int k = 0; k < N; ++k) x[k] = f4(v[k]);
-    // The NEG rule is decided per group of four; a scalar element may sit alone in its group.
-    TapeBody<N> me = *this;
+      for (int u = 0; u < U; ++u) dst[u] = x[u][0];
+      break;
+    case 1:
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[u] = x[u][N > 1 ? 1 : 0];
+      break;
+    case 2:
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[u] = x[u][N > 2 ? 2 : 0];
+      break;
+    default:
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[u] = x[u][N > 3 ? 3 : 0];
+      break;
+    }
+  }
+
+  __device__ __forceinline__ float eval(const float *v, uint64_t idx) const {
+    f4 x[1][N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) x[0][k] = f4(v[k]);
+    // a lone element decides the NEG rule for itself
+    TapeBody<N, TRIG> me = *this;
     me.simd_end = idx < simd_end ? ~uint64_t(0) : 0;
-    return me.eval4(x, 0)[0];
+    const uint64_t i0[1] = {0};
+    const bool ok[1] = {true};
+    f4 r[1];
+    me.template eval_units<1>(x, i0, ok, r);
+    return r[0][0];
   }
 };
 

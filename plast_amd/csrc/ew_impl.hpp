@@ -23,7 +23,6 @@ struct EwArgs {
   uint64_t shape64[kMaxRank];  // extents, for the 64-bit generic kernel
 };
 
-constexpr int kEwUnroll = 4;  // float4 units per lane per launch tile
 
 template <int NIN>
 __device__ __forceinline__ f4 load4(const EwArgs<NIN> &A, int k, int64_t off) {
@@ -38,6 +37,7 @@ __device__ __forceinline__ f4 load4(const EwArgs<NIN> &A, int k, int64_t off) {
 template <class Body, int ORANK>
 __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
+  constexpr int kEwUnroll = Body::kUnroll;
   const uint64_t base = uint64_t(blockIdx.x) * (kBlock * kEwUnroll) + threadIdx.x;
   f4 x[kEwUnroll][NIN];
   int64_t oo[kEwUnroll];
@@ -76,13 +76,18 @@ __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Bod
     for (int k = 0; k < NIN; ++k) x[u][k] = load4(A, k, off[k]);
     oo[u] = ooff;
   }
+  uint64_t idx[kEwUnroll];
+  bool valid[kEwUnroll];
 #pragma unroll
   for (int u = 0; u < kEwUnroll; ++u) {
-    const uint64_t q = base + uint64_t(u) * kBlock;
-    if (q >= A.units) continue;
-    const f4 r = body.eval4(x[u], q * 4);
-    __builtin_nontemporal_store(r, reinterpret_cast<f4 *>(A.out + oo[u]));
+    idx[u] = (base + uint64_t(u) * kBlock) * 4;
+    valid[u] = base + uint64_t(u) * kBlock < A.units;
   }
+  f4 r[kEwUnroll];
+  body.template eval_units<kEwUnroll>(x, idx, valid, r);
+#pragma unroll
+  for (int u = 0; u < kEwUnroll; ++u)
+    if (valid[u]) __builtin_nontemporal_store(r[u], reinterpret_cast<f4 *>(A.out + oo[u]));
 }
 
 // Generic kernel: any strides, one element per lane per step. IDX64 selects 64-bit division for
@@ -120,6 +125,177 @@ __global__ __launch_bounds__(kBlock) void ew_generic_kernel(EwArgs<Body::NIN> A,
     for (int k = 0; k < NIN; ++k) v[k] = A.in[k][off[k]];
     A.out[ooff] = body.eval(v, e);
   }
+}
+
+// Transposed-operand kernel. Some input is unit-stride along axis q while the output is
+// unit-stride along the innermost axis p. Each workgroup owns a 64x64 (q, p) tile of one batch
+// index: transposed inputs are read coalesced along q (float4) into LDS, then every output row is
+// produced coalesced along p (float4) with the other inputs read directly (float4 along p, or a
+// broadcast scalar). Requires extents of q and p divisible by 4 and 16-byte aligned rows.
+constexpr int kTile = 64;
+constexpr int kTilePad = 1;
+
+template <int NIN>
+struct TileArgs {
+  const float *in[NIN];
+  float *out;
+  int64_t bst[NIN + 1][kMaxRank];  // batch-axis strides (output last)
+  MagicDiv bdv[kMaxRank];
+  int nbatch;
+  int64_t qst[NIN + 1], pst[NIN + 1];
+  uint32_t eq, ep;                 // extents of q and p
+  uint32_t tq, tp;                 // tiles along q and p
+  uint32_t lds_mask;               // bit k: input k is staged through LDS
+  uint32_t lds_slot[NIN];
+  uint64_t row_stride_p_index;     // elements per unit of the output's q coordinate in idx terms
+};
+
+template <class Body>
+__global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, Body body) {
+  constexpr int NIN = Body::NIN;
+  extern __shared__ float lds[];
+  uint32_t bid = blockIdx.x;
+  const uint32_t tpi = bid % A.tp;
+  bid /= A.tp;
+  const uint32_t tqi = bid % A.tq;
+  uint32_t bi = bid / A.tq;
+  int64_t base[NIN + 1] = {};
+  for (int d = A.nbatch - 1; d >= 0; --d) {
+    const uint32_t nxt = A.bdv[d].div(bi);
+    const int64_t c = int64_t(bi - nxt * A.bdv[d].d);
+    bi = nxt;
+#pragma unroll
+    for (int k = 0; k <= NIN; ++k) base[k] += c * A.bst[k][d];
+  }
+  const uint32_t q0 = tqi * kTile, p0 = tpi * kTile;
+  const int t = threadIdx.x;
+  // stage: thread t loads float4 (along q) of rows b = t/16 + 16r of the tile
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) {
+    if (!(A.lds_mask >> k & 1u)) continue;
+    float *tile = lds + A.lds_slot[k] * (kTile * (kTile + kTilePad));
+    const uint32_t a4 = (t & 15) * 4;
+    f4 v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t b = (t >> 4) + 16 * r;
+      if (q0 + a4 < A.eq && p0 + b < A.ep)
+        v[r] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(
+            A.in[k] + base[k] + int64_t(q0 + a4) * A.qst[k] + int64_t(p0 + b) * A.pst[k]));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t b = (t >> 4) + 16 * r;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) tile[b * (kTile + kTilePad) + a4 + c] = v[r][c];
+    }
+  }
+  __syncthreads();
+  // produce: thread t writes float4 (along p) of output rows a = t/16 + 16r, two rows at a time
+  const uint32_t b4 = (t & 15) * 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    f4 x[2][NIN];
+    uint64_t idx[2] = {0, 0};  // the NEG rule never applies to a strided chain
+    bool valid[2];
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      const uint32_t a = (t >> 4) + 16 * (2 * h + r2);
+      valid[r2] = q0 + a < A.eq && p0 + b4 < A.ep;
+      if (!valid[r2]) continue;
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) {
+        if (A.lds_mask >> k & 1u) {
+          const float *tile = lds + A.lds_slot[k] * (kTile * (kTile + kTilePad));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) x[r2][k][c] = tile[(b4 + c) * (kTile + kTilePad) + a];
+        } else {
+          const float *src =
+              A.in[k] + base[k] + int64_t(q0 + a) * A.qst[k] + int64_t(p0 + b4) * A.pst[k];
+          x[r2][k] = A.pst[k] == 0 ? f4(src[0])
+                                   : __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src));
+        }
+      }
+    }
+    f4 res[2];
+    body.template eval_units<2>(x, idx, valid, res);
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      if (!valid[r2]) continue;
+      const uint32_t a = (t >> 4) + 16 * (2 * h + r2);
+      __builtin_nontemporal_store(
+          res[r2], reinterpret_cast<f4 *>(A.out + base[NIN] + int64_t(q0 + a) * A.qst[NIN] +
+                                          int64_t(p0 + b4)));
+    }
+  }
+}
+
+// Try the transposed-operand kernel on collapsed space `s`; false when the layout does not fit.
+template <class Body>
+bool try_tile(const Body &body, const void *const *in, void *out, const Space &s) {
+  constexpr int NIN = Body::NIN;
+  const int r = s.rank;
+  if (r < 2 || !aligned16(out) || s.st[NIN][r - 1] != 1) return false;
+  const int p = r - 1;
+  int q = -1;
+  for (int k = 0; k < NIN; ++k) {
+    const int64_t sp = s.st[k][p];
+    if (sp == 0 || sp == 1) continue;
+    int qk = -1;
+    for (int d = 0; d < p; ++d)
+      if (s.st[k][d] == 1) qk = d;
+    if (qk < 0 || (q >= 0 && qk != q)) return false;
+    q = qk;
+  }
+  if (q < 0) return false;
+  if (s.shape[p] % 4 || s.shape[q] % 4 || s.shape[p] >= (1u << 31) || s.shape[q] >= (1u << 31))
+    return false;
+  TileArgs<NIN> A;
+  memset(&A, 0, sizeof A);
+  uint32_t slots = 0;
+  for (int k = 0; k <= NIN; ++k) {
+    A.qst[k] = s.st[k][q];
+    A.pst[k] = s.st[k][p];
+    if (k < NIN) {
+      A.in[k] = static_cast<const float *>(in[k]);
+      const bool staged = A.pst[k] != 0 && A.pst[k] != 1;
+      const bool vec_ok = staged ? (A.pst[k] % 4 == 0 && aligned16(in[k]))
+                                 : (A.pst[k] == 0 || aligned16(in[k]));
+      if (!vec_ok) return false;
+      if (staged) {
+        A.lds_mask |= 1u << k;
+        A.lds_slot[k] = slots++;
+      } else if (A.pst[k] == 1 && A.qst[k] % 4 != 0) {
+        return false;
+      }
+    } else if (A.qst[k] % 4 != 0) {
+      return false;
+    }
+  }
+  uint64_t batch = 1;
+  int nb = 0;
+  for (int d = 0; d < p; ++d) {
+    if (d == q) continue;
+    for (int k = 0; k <= NIN; ++k) {
+      A.bst[k][nb] = s.st[k][d];
+      const bool f4_operand = k == NIN || !((A.lds_mask >> k & 1u) == 0 && A.pst[k] == 0);
+      if (f4_operand && s.st[k][d] % 4 != 0) return false;
+    }
+    A.bdv[nb] = MagicDiv::make(uint32_t(s.shape[d]));
+    batch *= s.shape[d];
+    ++nb;
+  }
+  A.nbatch = nb;
+  A.out = static_cast<float *>(out);
+  A.eq = uint32_t(s.shape[q]);
+  A.ep = uint32_t(s.shape[p]);
+  A.tq = ceil_div(A.eq, kTile);
+  A.tp = ceil_div(A.ep, kTile);
+  const uint64_t blocks = batch * A.tq * A.tp;
+  if (blocks >= (uint64_t(1) << 31)) return false;
+  const size_t lds_bytes = size_t(slots) * kTile * (kTile + kTilePad) * sizeof(float);
+  ew_tile_kernel<Body><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
+  return true;
 }
 
 // ------------------------------------------------------------------------- host dispatch
@@ -163,7 +339,7 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.units = n / 4;
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
-    const unsigned grid = ceil_div(A.units, uint64_t(kBlock) * kEwUnroll);
+    const unsigned grid = ceil_div(A.units, uint64_t(kBlock) * Body::kUnroll);
     switch (in_ax) {
     case 0: ew_vec_kernel<Body, 0><<<grid, kBlock, 0, stream()>>>(A, body); break;
     case 1: ew_vec_kernel<Body, 1><<<grid, kBlock, 0, stream()>>>(A, body); break;
@@ -172,6 +348,9 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     }
     return true;
   }
+
+  // --- transposed-operand path
+  if (n < (uint64_t(1) << 32) && try_tile(body, in, out, s)) return true;
 
   // --- generic path
   uint64_t blocks = (n + kBlock - 1) / kBlock;

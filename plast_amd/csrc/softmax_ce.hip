@@ -69,82 +69,6 @@ __device__ __forceinline__ float row_max_exact(float m, bool nan, const float *r
   return m > -FLT_MAX ? m : -FLT_MAX;
 }
 
-// Register-resident forward: each lane keeps NV float4 of the row, so the row is read from HBM once.
-template <int NV>
-__global__ __launch_bounds__(kCeBlock) void ce_fwd_reg_kernel(const float *__restrict__ x,
-                                                              const int32_t *__restrict__ lab,
-                                                              float *__restrict__ stats,
-                                                              float *__restrict__ loss, uint32_t C,
-                                                              uint64_t simd_end) {
-  __shared__ float lds[kCeWaves + 1];
-  const uint64_t row = blockIdx.x;
-  const float *xr = x + row * C;
-  const f4 *x4 = reinterpret_cast<const f4 *>(xr);
-  const uint32_t C4 = C / 4;
-  f4 v[NV];
-  float m = -__builtin_huge_valf();
-  bool nan = false;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
-    if (q < C4) {
-      v[i] = __builtin_nontemporal_load(x4 + q);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        m = fmaxf(m, v[i][c]);
-        nan = nan || v[i][c] != v[i][c];
-      }
-    }
-  }
-  const float mx = row_max_exact(m, nan, xr, C, lds);
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
-    if (q < C4) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s += expf(v[i][c] - mx);
-    }
-  }
-  s = block_sum(s, lds);
-  const float l = logf(s);
-  const int32_t y = lab[row];
-  bool bad = false;
-  float tl = 0.0f;
-  bool have = false;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint32_t q = threadIdx.x + uint32_t(i) * kCeBlock;
-    if (q < C4) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float ls = (v[i][c] - mx) - l;
-        const int32_t j = int32_t(q * 4 + c);
-        if (j == y) {
-          tl = ls;
-          have = true;
-        } else {
-          bad = bad || !(fabsf(ls) <= FLT_MAX);  // 0 * (NaN or inf) is NaN
-        }
-      }
-    }
-  }
-  bad = block_any(bad, lds);
-  if (have) {
-    const float t = bad ? __builtin_nanf("") : 0.0f + tl;
-    loss[row] = row < simd_end ? 0.0f - t : -t;
-    stats[2 * row] = mx;
-    stats[2 * row + 1] = l;
-  }
-  // a label outside [0, C) selects no term: t = +0 (or NaN)
-  if (threadIdx.x == 0 && (y < 0 || uint32_t(y) >= C)) {
-    const float t = bad ? __builtin_nanf("") : 0.0f;
-    loss[row] = row < simd_end ? 0.0f - t : -t;
-    stats[2 * row] = mx;
-    stats[2 * row + 1] = l;
-  }
-}
-
 // Any row length or alignment: three passes over the row (max, exp-sum, terms).
 __global__ __launch_bounds__(kCeBlock) void ce_fwd_generic_kernel(const float *__restrict__ x,
                                                                   const int32_t *__restrict__ lab,
@@ -183,44 +107,177 @@ __global__ __launch_bounds__(kCeBlock) void ce_fwd_generic_kernel(const float *_
   }
 }
 
-// Backward: grid (row chunks, rows); each lane handles float4s of one row.
-template <bool VEC, bool OVERWRITE>
-__global__ __launch_bounds__(kCeBlock) void ce_bwd_kernel(const float *__restrict__ x,
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m));
+  return v;
+}
+
+constexpr int kCeUnroll = 8;  // float4 loads in flight per lane
+
+// One wave64 per row, a single read of the row. Each lane keeps an online (max, exp-sum) pair,
+// rescaling its sum when its max grows; the wave merges the pairs. Rows for which the fast
+// values could differ from the reference chain's bits (a non-finite logit, a zero or non-finite
+// max, or a shifted-and-normalised logit that overflows to -inf) are recomputed exactly by the
+// same wave from memory.
+__global__ __launch_bounds__(256) void ce_fwd_wave_kernel(const float *__restrict__ x,
                                                           const int32_t *__restrict__ lab,
-                                                          const float *__restrict__ stats,
-                                                          const float *__restrict__ dloss,
-                                                          float *dx, uint32_t C,
-                                                          uint32_t per_block, uint32_t chunks) {
+                                                          float *__restrict__ stats,
+                                                          float *__restrict__ loss, uint64_t N,
+                                                          uint32_t C, uint64_t simd_end) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= N) return;  // whole wave
+  const float *xr = x + row * C;
+  const int32_t y = lab[row];
+  const float ninf = -__builtin_huge_valf();
+  float m = ninf, s = 0.0f, mn = __builtin_huge_valf();
+  bool nonfin = false;
+  const uint32_t C4 = C / 4;
+  const f4 *x4 = reinterpret_cast<const f4 *>(xr);
+  for (uint32_t q0 = lane; q0 < C4; q0 += 64 * kCeUnroll) {
+    f4 v[kCeUnroll];
+#pragma unroll
+    for (int u = 0; u < kCeUnroll; ++u) {
+      const uint32_t q = q0 + uint32_t(u) * 64;
+      if (q < C4) v[u] = __builtin_nontemporal_load(x4 + q);
+    }
+#pragma unroll
+    for (int u = 0; u < kCeUnroll; ++u) {
+      if (q0 + uint32_t(u) * 64 >= C4) continue;
+      const float g = fmaxf(fmaxf(v[u][0], v[u][1]), fmaxf(v[u][2], v[u][3]));
+      if (g > m) {
+        s = s * expf(m - g);
+        m = g;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float e = v[u][c];
+        nonfin = nonfin || !(fabsf(e) <= FLT_MAX);
+        mn = fminf(mn, e);
+        s += expf(e - m);
+      }
+    }
+  }
+  nonfin = __any(nonfin);
+  const float M = wave_max(m);
+  const float sc = m == ninf ? 0.0f : s * expf(m - M);
+  float S = wave_sum(sc);
+  mn = wave_min(mn);
+  float mx = M;
+  bool exact = false;
+  if (!(fabsf(M) <= FLT_MAX) || M == 0.0f || nonfin) {
+    exact = true;
+  }
+  float l = logf(S);
+  if (!exact && C > 0) {
+    // the most negative shifted-normalised logit must stay finite (else 0 * -inf = NaN)
+    if (!(fabsf((mn - mx) - l) <= FLT_MAX)) exact = true;
+  }
+  bool bad = false;
+  if (exact) {
+    // the reference chain, element by element (rare rows)
+    float acc = -FLT_MAX;
+    if (lane == 0)
+      for (uint32_t j = 0; j < C; ++j) acc = acc > xr[j] ? acc : xr[j];
+    mx = __shfl(acc, 0);
+    float t = 0.0f;
+    for (uint32_t j = lane; j < C; j += 64) t += expf(xr[j] - mx);
+    S = wave_sum(t);
+    l = logf(S);
+    bool b = false;
+    for (uint32_t j = lane; j < C; j += 64) {
+      const float ls = (xr[j] - mx) - l;
+      if (int32_t(j) != y) b = b || !(fabsf(ls) <= FLT_MAX);
+    }
+    bad = __any(b);
+  }
+  if (lane == 0) {
+    float t;
+    if (bad) t = __builtin_nanf("");
+    else if (y >= 0 && uint32_t(y) < C) t = 0.0f + ((xr[y] - mx) - l);
+    else t = 0.0f;
+    loss[row] = row < simd_end ? 0.0f - t : -t;
+    stats[2 * row] = mx;
+    stats[2 * row + 1] = l;
+  }
+}
+
+// Backward, float4 path: a workgroup owns kBwdUnroll float4 per lane of one row; all of a lane's
+// loads are issued before any arithmetic.
+constexpr int kBwdUnroll = 4;
+
+template <bool OVERWRITE>
+__global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__restrict__ x,
+                                                              const int32_t *__restrict__ lab,
+                                                              const float *__restrict__ stats,
+                                                              const float *__restrict__ dloss,
+                                                              float *dx, uint32_t C, uint32_t chunks) {
   const uint64_t row = blockIdx.x / chunks;
   const uint32_t chunk = blockIdx.x - uint32_t(row) * chunks;
   const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
   const int32_t y = lab[row];
-  const uint32_t j0 = chunk * per_block;
-  const uint32_t j1 = j0 + per_block < C ? j0 + per_block : C;
+  const uint32_t C4 = C / 4;
+  const f4 *x4 = reinterpret_cast<const f4 *>(x + row * C);
+  f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
+  const uint32_t q0 = chunk * (kCeBlock * kBwdUnroll) + threadIdx.x;
+  f4 xv[kBwdUnroll], dv[kBwdUnroll];
+#pragma unroll
+  for (int u = 0; u < kBwdUnroll; ++u) {
+    const uint32_t q = q0 + uint32_t(u) * kCeBlock;
+    if (q < C4) {
+      xv[u] = __builtin_nontemporal_load(x4 + q);
+      if constexpr (!OVERWRITE) dv[u] = __builtin_nontemporal_load(d4 + q);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kBwdUnroll; ++u) {
+    const uint32_t q = q0 + uint32_t(u) * kCeBlock;
+    if (q >= C4) continue;
+    f4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float sm = expf((xv[u][c] - m) - l);
+      const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
+      const float gv = g * (sm - oh);
+      if constexpr (OVERWRITE) r[c] = gv;
+      else r[c] = dv[u][c] + gv;
+    }
+    __builtin_nontemporal_store(r, d4 + q);
+  }
+}
+
+// Backward, any alignment: one element per lane per step.
+template <bool OVERWRITE>
+__global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__restrict__ x,
+                                                                 const int32_t *__restrict__ lab,
+                                                                 const float *__restrict__ stats,
+                                                                 const float *__restrict__ dloss,
+                                                                 float *dx, uint32_t C,
+                                                                 uint32_t chunks) {
+  const uint64_t row = blockIdx.x / chunks;
+  const uint32_t chunk = blockIdx.x - uint32_t(row) * chunks;
+  const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
+  const int32_t y = lab[row];
   const float *xr = x + row * C;
   float *dr = dx + row * C;
-  if constexpr (VEC) {
-    for (uint32_t j = j0 + threadIdx.x * 4; j < j1; j += kCeBlock * 4) {
-      const f4 xv = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + j));
-      f4 d;
-      if constexpr (!OVERWRITE) d = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(dr + j));
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float sm = expf((xv[c] - m) - l);
-        const float oh = int32_t(j + c) == y ? 1.0f : 0.0f;
-        const float gv = g * (sm - oh);
-        if constexpr (OVERWRITE) d[c] = gv;
-        else d[c] = d[c] + gv;
-      }
-      __builtin_nontemporal_store(d, reinterpret_cast<f4 *>(dr + j));
-    }
-  } else {
-    for (uint32_t j = j0 + threadIdx.x; j < j1; j += kCeBlock) {
-      const float sm = expf((xr[j] - m) - l);
-      const float oh = int32_t(j) == y ? 1.0f : 0.0f;
-      const float gv = g * (sm - oh);
-      dr[j] = OVERWRITE ? gv : dr[j] + gv;
-    }
+  const uint32_t j0 = chunk * (kCeBlock * kBwdUnroll * 4);
+  const uint32_t j1 = j0 + kCeBlock * kBwdUnroll * 4 < C ? j0 + kCeBlock * kBwdUnroll * 4 : C;
+  for (uint32_t j = j0 + threadIdx.x; j < j1; j += kCeBlock) {
+    const float sm = expf((xr[j] - m) - l);
+    const float oh = int32_t(j) == y ? 1.0f : 0.0f;
+    const float gv = g * (sm - oh);
+    dr[j] = OVERWRITE ? gv : dr[j] + gv;
   }
 }
 
@@ -277,12 +334,9 @@ void softmax_cross_entropy_hip_forward(const Tensor **inputs, Tensor *output, Ke
   const bool vec = C % 4 == 0 && aligned16(px) && C > 0;
   const uint32_t C4 = C / 4;
   const unsigned grid = unsigned(N);
-  if (vec && C4 <= kCeBlock * 8)
-    ce_fwd_reg_kernel<8><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
-  else if (vec && C4 <= kCeBlock * 16)
-    ce_fwd_reg_kernel<16><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
-  else if (vec && C4 <= kCeBlock * 32)
-    ce_fwd_reg_kernel<32><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  (void)C4;
+  if (vec)
+    ce_fwd_wave_kernel<<<ceil_div(N, 4), 256, 0, stream()>>>(px, pl, ps, po, N, C, se);
   else
     ce_fwd_generic_kernel<<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
   finish(where);
@@ -308,8 +362,8 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
   const float *px = static_cast<const float *>(x->data);
   float *pd = static_cast<float *>(x->grad->data);
   const bool vec = C % 4 == 0 && aligned16(px) && aligned16(pd);
-  // each workgroup covers 8 float4 per lane of one row
-  const uint32_t per_block = kCeBlock * 4 * 8;
+  // each workgroup covers kBwdUnroll float4 per lane of one row
+  const uint32_t per_block = kCeBlock * kBwdUnroll * 4;
   const uint32_t chunks = ceil_div(C, per_block);
   if (uint64_t(chunks) * N >= (uint64_t(1) << 31)) {
     report_error(where, "more than 2^31 workgroups");
@@ -321,13 +375,13 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
   const float *pg = static_cast<const float *>(output->grad->data);
   const bool over = params.keepdim == 1;
   if (vec && over)
-    ce_bwd_kernel<true, true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+    ce_bwd_vec_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   else if (vec)
-    ce_bwd_kernel<true, false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+    ce_bwd_vec_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   else if (over)
-    ce_bwd_kernel<false, true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+    ce_bwd_scalar_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   else
-    ce_bwd_kernel<false, false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, per_block, chunks);
+    ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   finish(where);
 }
 

@@ -313,3 +313,22 @@ def assert_close_sum(x, y, scale, rel=1e-5, what=""):
         i = np.argwhere(~ok)[0]
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} out of tolerance; first at "
                              f"{tuple(i)}: {x[tuple(i)]!r} vs {y[tuple(i)]!r} (scale {np.asarray(scale)[tuple(i)] if np.ndim(scale) else scale})")
+
+
+def assert_sum_parity(gpu, ref, truth, scale, rel=1e-5, what=""):
+    """Parity for a reordered fp32 sum: within rel*scale of the reference's serial sum, or - where
+    the serial sum itself has drifted further than that from the exact (fp64) value - at least as
+    close to the exact value as the reference is."""
+    g = np.asarray(gpu, np.float64)
+    r = np.asarray(ref, np.float64)
+    t = np.asarray(truth, np.float64)
+    sc = np.asarray(scale, np.float64)
+    both_nan = np.isnan(g) & np.isnan(r)
+    same_inf = np.isinf(g) & (g == r)
+    near_ref = np.abs(g - r) <= rel * np.maximum(sc, 1e-30)
+    better = np.abs(g - t) <= np.maximum(np.abs(r - t), rel * sc)
+    ok = both_nan | same_inf | near_ref | better
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} fail; first at {tuple(i)}: "
+                             f"gpu {g[tuple(i)]!r} ref {r[tuple(i)]!r} exact {t[tuple(i)]!r}")
