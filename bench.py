@@ -108,7 +108,8 @@ class C2Fused(Workload):
         self.g.forward()
 
     def check(self, k=1 << 20):
-        """Parity of the first k outputs with the oracle (bench-side sanity check)."""
+        """Max ulp distance of the first k outputs from the oracle (bench-side sanity check; the
+        chain's only inexact op is exp, allowed 2 ulp)."""
         sys.path.insert(0, str(ROOT / "tests"))
         from hostlib import fused_chain2
         a = self.a.numpy()[:k]
@@ -116,8 +117,8 @@ class C2Fused(Workload):
         c = self.c.numpy()[:k]
         want = fused_chain2(a, b, c)
         got = self.y.numpy()[:k]
-        same = (got.view(np.uint32) == want.view(np.uint32)).mean()
-        return float(same)
+        ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+        return int(ulp.max())
 
     def cpu(self, reps=3):
         """The reference's unfused chain (MUL, ADD, LEAKY_RELU, NEG, EXP) through its CPU kernels."""
@@ -329,7 +330,9 @@ def main(argv=None) -> int:
     ms = timed(head.step, a.steps, a.warmup)
     gbs = head.bytes_per_call / (ms * 1e-3) / 1e9
     same = head.check()
-    log(f"config2 fused: {ms:.4f} ms/step, {gbs:.1f} GB/s, parity (first 1M, bit-equal) = {same}")
+    log(f"config2 fused: {ms:.4f} ms/step, {gbs:.1f} GB/s, parity (first 1M) max ulp = {same}")
+    if same > 2:
+        raise SystemExit(f"bench.py: config 2 output differs from the oracle by {same} ulp")
 
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
@@ -357,7 +360,7 @@ def main(argv=None) -> int:
                 log(f"{w.name}: ERROR {e}")
             finally:
                 w.free()
-    head_detail = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "parity_first_1M_bit_equal": same,
+    head_detail = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "parity_first_1M_max_ulp": same,
                    "launches_per_step": len(head.kinds)}
 
     line = {

@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 from cases import CASES, assert_bits, assert_close_sum, materialize, run_case
-from hostlib import (HostBackend, HostTensor, libm_expf, oracle_backward, oracle_forward,
-                     ref_available, ref_ce_chain)
+from hostlib import (HostBackend, HostTensor, fused_chain2, libm_expf, oracle_backward,
+                     oracle_forward, ref_available, ref_ce_chain, ref_forward)
 from plast_amd.abi import DIM_ALL, KernelParams
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_cases.npz"
@@ -147,6 +147,47 @@ def test_softmax_ce_invariants():
     O.grad.buf[:] = 1.0
     oracle_backward("softmax_cross_entropy", [X, L, S], O)
     np.testing.assert_allclose(X.grad.numpy().sum(1), 0.0, atol=1e-5)
+
+
+def _chain2_by_ops(fwd, a, b, c):
+    """Config 2's chain as the reference runs it unfused: MUL, ADD, LEAKY_RELU(0), NEG, EXP, each a
+    separate op over contiguous [n] tensors (five nodes of the reference DAG)."""
+    n = a.size
+    A, B, Cc = HostTensor(a), HostTensor(b), HostTensor(c)
+    T = [HostTensor(np.zeros(n, np.float32)) for _ in range(5)]
+    fwd("mul", [A, B], T[0])
+    fwd("add", [T[0], Cc], T[1])
+    fwd("leaky_relu", [T[1]], T[2], KernelParams(0, 0, 0.0))
+    fwd("neg", [T[2]], T[3])
+    fwd("exp", [T[3]], T[4])
+    return T[4].numpy()
+
+
+def _chain2_inputs(n, seed):
+    rng = np.random.RandomState(seed)
+    a, b, c = (rng.randn(n).astype(np.float32) for _ in range(3))
+    # specials: signed zeros into relu (-> -0.0, then neg -> +0/-0 by the SIMD rule), infinities,
+    # NaN and values whose exp under/overflows
+    sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 100.0, -100.0, 1e-30], np.float32)
+    k = min(n, sp.size)
+    a[:k] = sp[:k]
+    c[:k] = -sp[:k]
+    return a, b, c
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 13, 4096, 100_003])
+def test_chain2_oracle_equals_its_pinned_ops(n):
+    """oracle_fused_chain2 is bit-identical to the oracle's own MUL/ADD/LEAKY_RELU/NEG/EXP kernels,
+    each of which is pinned to the golden vectors; n covers the NEG rule's SIMD block and tail."""
+    a, b, c = _chain2_inputs(n, n)
+    assert_bits(fused_chain2(a, b, c), _chain2_by_ops(oracle_forward, a, b, c), "chain vs ops")
+
+
+@pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("n", [1, 13, 100_003])
+def test_chain2_oracle_equals_reference_chain(n):
+    a, b, c = _chain2_inputs(n, 7 * n + 1)
+    assert_bits(fused_chain2(a, b, c), _chain2_by_ops(ref_forward, a, b, c), "chain vs reference")
 
 
 def test_planted_mistake_is_caught():
