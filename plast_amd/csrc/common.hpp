@@ -15,6 +15,26 @@ namespace plast {
 constexpr int kMaxRank = PLAST_MAX_NDIM;
 constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 wave64s)
 
+// Launch-shape knobs, measured on MI355X (overridable with -D for sweeps).
+#ifndef PLAST_EW_UNROLL
+#define PLAST_EW_UNROLL 4    // float4 units per lane, fixed elementwise bodies
+#endif
+#ifndef PLAST_TAPE_UNROLL
+#define PLAST_TAPE_UNROLL 2  // float4 units per lane, fused-chain interpreter
+#endif
+#ifndef PLAST_ROW_UNROLL
+#define PLAST_ROW_UNROLL 4   // float4 loads in flight per lane, row reductions
+#endif
+#ifndef PLAST_COL_UNROLL
+#define PLAST_COL_UNROLL 4   // rows in flight per lane, leading-axis reductions
+#endif
+#ifndef PLAST_COL_BLOCKS
+#define PLAST_COL_BLOCKS 1024  // workgroups a leading-axis reduction is chunked up to
+#endif
+#ifndef PLAST_CE_BWD_UNROLL
+#define PLAST_CE_BWD_UNROLL 1  // float4 units per lane, cross-entropy backward
+#endif
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------- runtime / errors

@@ -78,7 +78,7 @@ __device__ __forceinline__ float grad_b(float g, float x, float y, bool simd) {
 
 template <class Derived>
 struct ScalarBody {
-  static constexpr int kUnroll = 4;  // float4 units per lane
+  static constexpr int kUnroll = PLAST_EW_UNROLL;  // float4 units per lane
   template <int U, int N>
   __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
                                              const bool (&valid)[U], f4 (&acc)[U]) const {
@@ -173,7 +173,7 @@ struct AccumDivBody : ScalarBody<AccumDivBody> {
 template <int N, bool TRIG>
 struct TapeBody {
   static constexpr int NIN = N;
-  static constexpr int kUnroll = 2;  // float4 units per lane: keeps the interpreter under 64 VGPRs
+  static constexpr int kUnroll = PLAST_TAPE_UNROLL;  // float4 units per lane (keeps the interpreter under 64 VGPRs)
   PlastFusedTape t;
   uint64_t simd_end;
 

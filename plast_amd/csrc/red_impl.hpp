@@ -246,7 +246,7 @@ __device__ ExtPart exact_range(const RedArgs<NIN> &A, const Prod &prod, const in
   return ExtPart{r, kNonEmpty | (last_nan >= 0 ? kIndep : 0u)};
 }
 
-constexpr int kRowUnroll = 4;  // float4 loads in flight per lane per operand
+constexpr int kRowUnroll = PLAST_ROW_UNROLL;  // float4 loads in flight per lane per operand
 
 template <class Prod, class Comb, bool VEC>
 __global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, Prod prod) {
@@ -374,18 +374,37 @@ __global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
 
 // ------------------------------------------------------------------------- cols kernel
 
-constexpr int kColUnroll = 4;
+constexpr int kColUnroll = PLAST_COL_UNROLL;
 
-// grid.x: (outer index, block of kBlock lanes along the kept innermost axis); grid.y: chunk.
+// Fast summary of an order-sensitive fold (exact max/min): the plain extreme and a NaN flag.
+struct ExtFast {
+  float m;
+  uint32_t nan;
+};
+
+// grid.x: (outer index, slice of 64 lanes x W columns of the kept innermost axis); grid.y: chunk
+// of the reduced axis. The workgroup's four waves take interleaved rows of the chunk (wave w reads
+// rows k0 + w, k0 + w + 4, ...), so each wave streams its own rows while the workgroup still
+// covers one contiguous slice per row; each lane owns W adjacent columns. The four partials of a
+// column combine through LDS in wave order (deterministic). Order-free combiners (sum, argmax)
+// merge directly. The exact max/min fold keeps a plain extreme and a NaN flag per wave, and a
+// column is refolded serially in index order only when its chunk holds a NaN or its extreme is
+// zero (the cases where order decides the bits).
 template <class Prod, class Comb, bool VEC>
 __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, Prod prod,
                                                           uint32_t xblocks) {
   constexpr int NIN = Prod::NIN;
   constexpr int W = VEC ? 4 : 1;
   using Part = typename Comb::Part;
+  constexpr bool kExt = Comb::kExact;
+  constexpr bool IS_MAX = std::is_same<Comb, ExtComb<true>>::value;
+  using Fast = typename std::conditional<kExt, ExtFast, Part>::type;
+  __shared__ Fast sh[kBlock / 64][64 * W];
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint32_t o = blockIdx.x / xblocks;
-  const uint64_t j = (uint64_t(blockIdx.x - o * xblocks) * kBlock + threadIdx.x) * W;
-  if (j >= A.inner) return;
+  const uint64_t j = (uint64_t(blockIdx.x - o * xblocks) * 64 + lane) * W;
+  const bool active = j < A.inner;  // no early return: the workgroup meets at a barrier
   const uint32_t chunk = blockIdx.y;
   int64_t base[NIN], tbase;
   decode_outer(A, o, base, tbase);
@@ -394,20 +413,25 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   const uint64_t k0 = uint64_t(chunk) * A.seglen;
   const uint64_t k1 = k0 + A.seglen < A.len ? k0 + A.seglen : A.len;
 
-  Part p[W];
+  Fast f[W];
 #pragma unroll
-  for (int c = 0; c < W; ++c) p[c] = Comb::empty();
-  for (uint64_t r0 = k0; r0 < k1; r0 += kColUnroll) {
+  for (int c = 0; c < W; ++c) {
+    if constexpr (kExt) f[c] = Fast{IS_MAX ? -__builtin_huge_valf() : __builtin_huge_valf(), 0u};
+    else f[c] = Comb::empty();
+  }
+  for (uint64_t r0 = k0 + wv; r0 < k1; r0 += 4 * kColUnroll) {
     float xv[kColUnroll][NIN][W];
 #pragma unroll
     for (int u = 0; u < kColUnroll; ++u) {
-      const uint64_t r = r0 + u;
-      if (r >= k1) continue;
+      const uint64_t r = r0 + 4 * u;
+      if (!active || r >= k1) continue;
 #pragma unroll
       for (int k = 0; k < NIN; ++k) {
         const float *src = A.in[k] + base[k] + int64_t(r) * A.rst[k];
         if constexpr (VEC) {
-          const f4 v = (A.vec_mask >> k & 1u) ? *reinterpret_cast<const f4 *>(src) : f4(src[0]);
+          const f4 v = (A.vec_mask >> k & 1u)
+                           ? __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src))
+                           : f4(src[0]);
 #pragma unroll
           for (int c = 0; c < W; ++c) xv[u][k][c] = v[c];
         } else {
@@ -417,27 +441,64 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
     }
 #pragma unroll
     for (int u = 0; u < kColUnroll; ++u) {
-      const uint64_t r = r0 + u;
-      if (r >= k1) continue;
+      const uint64_t r = r0 + 4 * u;
+      if (!active || r >= k1) continue;
 #pragma unroll
       for (int c = 0; c < W; ++c) {
         float v[NIN];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
         const float y = prod.eval(v);
-        if (r == k0) Comb::first(p[c], y, int64_t(r));
-        else Comb::next(p[c], y, int64_t(r));
+        if constexpr (kExt) {
+          f[c].m = IS_MAX ? fmaxf(f[c].m, y) : fminf(f[c].m, y);
+          f[c].nan |= y != y ? 1u : 0u;
+        } else {
+          Comb::next(f[c], y, int64_t(r));
+        }
       }
     }
   }
-  const uint64_t nout_inner = A.inner;
+#pragma unroll
+  for (int c = 0; c < W; ++c) sh[wv][lane * W + c] = f[c];
+  __syncthreads();
+  if (wv != 0 || !active) return;
+
 #pragma unroll
   for (int c = 0; c < W; ++c) {
-    if (A.segs == 1) {
-      store_final<Comb>(A.out, tbase + int64_t(j + c) * A.tkst, p[c], A.post, A.divisor);
+    Part p;
+    if constexpr (kExt) {
+      float m = sh[0][lane * W + c].m;
+      uint32_t nan = sh[0][lane * W + c].nan;
+#pragma unroll
+      for (int w = 1; w < kBlock / 64; ++w) {
+        m = IS_MAX ? fmaxf(m, sh[w][lane * W + c].m) : fminf(m, sh[w][lane * W + c].m);
+        nan |= sh[w][lane * W + c].nan;
+      }
+      if (!nan && m != 0.0f) {
+        p = ExtPart{m, kNonEmpty};
+      } else {
+        // the reference's fold over [k0, k1) in index order
+        p = Comb::empty();
+        for (uint64_t r = k0; r < k1; ++r) {
+          float v[NIN];
+#pragma unroll
+          for (int k = 0; k < NIN; ++k)
+            v[k] = A.in[k][base[k] + int64_t(c) * A.kst[k] + int64_t(r) * A.rst[k]];
+          const float y = prod.eval(v);
+          if (r == k0) Comb::first(p, y, int64_t(r));
+          else Comb::next(p, y, int64_t(r));
+        }
+      }
     } else {
-      const uint64_t oi = uint64_t(o) * nout_inner + j + c;
-      static_cast<Part *>(A.part)[uint64_t(chunk) * (A.rows * nout_inner) + oi] = p[c];
+      p = sh[0][lane * W + c];
+#pragma unroll
+      for (int w = 1; w < kBlock / 64; ++w) p = Comb::merge(p, sh[w][lane * W + c]);
+    }
+    if (A.segs == 1) {
+      store_final<Comb>(A.out, tbase + int64_t(j + c) * A.tkst, p, A.post, A.divisor);
+    } else {
+      const uint64_t oi = uint64_t(o) * A.inner + j + c;
+      static_cast<Part *>(A.part)[uint64_t(chunk) * (A.rows * A.inner) + oi] = p;
     }
   }
 }
@@ -671,12 +732,13 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
     }
     A.rows = nout / A.inner;  // outer count
     const uint32_t W = vec ? 4 : 1;
-    const uint32_t xblocks = ceil_div(A.inner, uint64_t(kBlock) * W);
+    const uint32_t xblocks = ceil_div(A.inner, uint64_t(64) * W);
     const uint64_t base_blocks = uint64_t(xblocks) * A.rows;
-    // chunk the reduced axis until the grid has ~2048 workgroups, keeping >= 64 rows per chunk
+    // chunk the reduced axis until the grid has ~PLAST_COL_BLOCKS workgroups, keeping >= 64 rows
+    // per chunk
     uint64_t chunks = 1;
-    if (base_blocks < 2048 && A.len >= 128) {
-      chunks = (2048 + base_blocks - 1) / base_blocks;
+    if (base_blocks < PLAST_COL_BLOCKS && A.len >= 128) {
+      chunks = (PLAST_COL_BLOCKS + base_blocks - 1) / base_blocks;
       const uint64_t max_c = A.len / 64;
       if (chunks > max_c) chunks = max_c;
       if (chunks > 65535) chunks = 65535;

@@ -8,7 +8,8 @@
 //   t = 0 + ((x_label - m) - l), or NaN when any other term 0 * ((x_j - m) - l) is NaN
 //   loss = 0 - t inside the reference's SIMD blocks of its NEG node, -t in its tail
 // stats[row] = (m, l) for the backward.
-// Backward: dx[row, j] (+)= dloss[row] * (expf((x - m) - l) - onehot).
+// Backward: dx[row, j] (+)= dloss[row] * (exp((x - m) - l) - onehot).
+// The fast paths evaluate exp with exp_le0 (about 1 ulp); the exact-refold paths use expf.
 #include <cfloat>
 
 #include "common.hpp"
@@ -18,6 +19,24 @@ namespace {
 
 constexpr int kCeBlock = 256;
 constexpr int kCeWaves = kCeBlock / 64;
+
+// exp(t) for the shifted logits of a softmax (t <= 0), from the hardware base-2 exponential
+// (v_exp_f32, accurate to 1 ulp). t*log2(e) is carried as p + d: p = t*L rounded, d = that
+// product's rounding error (one FMA) plus t times the error of L itself, so
+// exp(t) = 2^p * 2^d with 2^d = 1 + d*ln2 (|d| < 2^-17 for |t| < 87). About 1 ulp from the
+// correctly rounded result; 6 VALU ops where the library expf takes about 15. Below t = -87 the
+// result would be subnormal (< 2^-125.5) and 0 is returned; -inf gives 0 and NaN stays NaN.
+// Used only where the result feeds a sum or a gradient compared to 1e-5 relative.
+__device__ __forceinline__ float exp_le0(float t) {
+  constexpr float kL = 1.44269502162933349609375f;   // log2(e) rounded to fp32
+  constexpr float kLlo = 1.925963033500011079e-8f;   // log2(e) - kL
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float p = t * kL;
+  const float d = __builtin_fmaf(t, kLlo, __builtin_fmaf(t, kL, -p));
+  const float r = __builtin_amdgcn_exp2f(p);
+  const float e = __builtin_fmaf(r, d * kLn2, r);
+  return t < -87.0f ? 0.0f : e;
+}
 
 __device__ __forceinline__ float block_sum(float v, float *lds) {
 #pragma unroll
@@ -142,7 +161,6 @@ __global__ __launch_bounds__(256) void ce_fwd_wave_kernel(const float *__restric
   const int32_t y = lab[row];
   const float ninf = -__builtin_huge_valf();
   float m = ninf, s = 0.0f, mn = __builtin_huge_valf();
-  bool nonfin = false;
   const uint32_t C4 = C / 4;
   const f4 *x4 = reinterpret_cast<const f4 *>(xr);
   for (uint32_t q0 = lane; q0 < C4; q0 += 64 * kCeUnroll) {
@@ -157,22 +175,23 @@ __global__ __launch_bounds__(256) void ce_fwd_wave_kernel(const float *__restric
       if (q0 + uint32_t(u) * 64 >= C4) continue;
       const float g = fmaxf(fmaxf(v[u][0], v[u][1]), fmaxf(v[u][2], v[u][3]));
       if (g > m) {
-        s = s * expf(m - g);
+        s = m == ninf ? s * 0.0f : s * exp_le0(m - g);
         m = g;
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float e = v[u][c];
-        nonfin = nonfin || !(fabsf(e) <= FLT_MAX);
         mn = fminf(mn, e);
-        s += expf(e - m);
+        s += exp_le0(e - m);
       }
     }
   }
-  nonfin = __any(nonfin);
   const float M = wave_max(m);
-  const float sc = m == ninf ? 0.0f : s * expf(m - M);
+  const float sc = m == ninf ? s * 0.0f : s * exp_le0(m - M);
   float S = wave_sum(sc);
+  // a NaN logit reaches the sum (fmaxf skips NaN, exp(NaN - m) does not); an infinite one makes
+  // M or the minimum below non-finite
+  const bool nonfin = !(S <= FLT_MAX);
   mn = wave_min(mn);
   float mx = M;
   bool exact = false;
@@ -215,7 +234,7 @@ __global__ __launch_bounds__(256) void ce_fwd_wave_kernel(const float *__restric
 
 // Backward, float4 path: a workgroup owns kBwdUnroll float4 per lane of one row; all of a lane's
 // loads are issued before any arithmetic.
-constexpr int kBwdUnroll = 4;
+constexpr int kBwdUnroll = PLAST_CE_BWD_UNROLL;
 
 template <bool OVERWRITE>
 __global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__restrict__ x,
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__res
     f4 r;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float sm = expf((xv[u][c] - m) - l);
+      const float sm = exp_le0((xv[u][c] - m) - l);
       const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
       const float gv = g * (sm - oh);
       if constexpr (OVERWRITE) r[c] = gv;
@@ -274,7 +293,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
   const uint32_t j0 = chunk * (kCeBlock * kBwdUnroll * 4);
   const uint32_t j1 = j0 + kCeBlock * kBwdUnroll * 4 < C ? j0 + kCeBlock * kBwdUnroll * 4 : C;
   for (uint32_t j = j0 + threadIdx.x; j < j1; j += kCeBlock) {
-    const float sm = expf((xr[j] - m) - l);
+    const float sm = exp_le0((xr[j] - m) - l);
     const float oh = int32_t(j) == y ? 1.0f : 0.0f;
     const float gv = g * (sm - oh);
     dr[j] = OVERWRITE ? gv : dr[j] + gv;
