@@ -31,11 +31,31 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_COL_BLOCKS
 #define PLAST_COL_BLOCKS 1024  // workgroups a leading-axis reduction is chunked up to
 #endif
+// Store policy per kernel family (1: nontemporal, 0: ordinary stores).
+#ifndef PLAST_EW_NT_STORE
+#define PLAST_EW_NT_STORE -1  // -1: nontemporal exactly when the launch re-reads an operand
+#endif
+#ifndef PLAST_TILE_NT_STORE
+#define PLAST_TILE_NT_STORE 0
+#endif
+#ifndef PLAST_CE_NT_STORE
+#define PLAST_CE_NT_STORE 1
+#endif
+#ifndef PLAST_COPY_NT_STORE
+#define PLAST_COPY_NT_STORE 0
+#endif
 #ifndef PLAST_CE_BWD_UNROLL
 #define PLAST_CE_BWD_UNROLL 1  // float4 units per lane, cross-entropy backward
 #endif
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Store of a streamed float4 result with a compile-time cache policy.
+template <bool NT>
+__device__ __forceinline__ void store_stream(f4 v, f4 *p) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
 
 // ------------------------------------------------------------------------- runtime / errors
 

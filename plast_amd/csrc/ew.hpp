@@ -189,18 +189,22 @@ struct TapeBody {
   __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
                                              const bool (&valid)[U], f4 (&acc)[U]) const {
     (void)valid;
-    uint2 w0;
-    __builtin_memcpy(&w0, &t.ins[0], sizeof w0);
-    select_input(x, int((w0.x >> 16) & 0xffu), acc);
-    // not unrolled: the loop sits outside any lane-divergent branch, so i stays uniform and
-    // every t.ins[i] field is an SGPR-offset scalar load
+    // The tape's 2 * PLAST_TAPE_MAX_INS dwords, one per lane (lane 2i: op/src/idx/acc_rhs bytes of
+    // instruction i; lane 2i+1: its immediate), read back with v_readlane. A scalar load per
+    // instruction would need a wait on the shared scalar/LDS counter, which also drains a tile
+    // kernel's outstanding LDS reads.
+    static_assert(sizeof(PlastTapeIns) == 8, "tape instruction is two dwords");
+    const uint32_t words =
+        reinterpret_cast<const uint32_t *>(t.ins)[__lane_id() & (2 * PLAST_TAPE_MAX_INS - 1)];
+    const uint32_t w0x = uint32_t(__builtin_amdgcn_readlane(int(words), 0));
+    select_input(x, int((w0x >> 16) & 0xffu), acc);
+    // not unrolled: the loop sits outside any lane-divergent branch, so i stays uniform
     for (uint32_t i = 1; i < t.num_ins; ++i) {
-      // one 8-byte scalar load per instruction (scalar loads are dword-granular)
-      uint2 w;
-      __builtin_memcpy(&w, &t.ins[i], sizeof w);
-      const int op = int(w.x & 0xffu), src = int((w.x >> 8) & 0xffu), k = int((w.x >> 16) & 0xffu);
-      const bool rhs = (w.x >> 24) != 0u;
-      const float imm = __uint_as_float(w.y);
+      const uint32_t wx = uint32_t(__builtin_amdgcn_readlane(int(words), int(2 * i)));
+      const uint32_t wy = uint32_t(__builtin_amdgcn_readlane(int(words), int(2 * i + 1)));
+      const int op = int(wx & 0xffu), src = int((wx >> 8) & 0xffu), k = int((wx >> 16) & 0xffu);
+      const bool rhs = (wx >> 24) != 0u;
+      const float imm = __uint_as_float(wy);
       f4 o[U];
       if (src == TAPE_SRC_INPUT) {
         select_input(x, k, o);

@@ -17,6 +17,7 @@ struct EwArgs {
   MagicDiv dv[kMaxRank];  // divisors for the outer axes (vec kernel) or every axis (generic)
   int rank;
   uint32_t bcast_inner;   // bit k: input k has stride 0 on the innermost axis
+  uint32_t reused;        // bit k: input k has stride 0 on some axis (re-read: cached loads)
   uint64_t n;             // elements in the space
   uint64_t units;         // float4 units (vec kernel)
   MagicDiv dinner4;       // innermost extent / 4 (vec kernel)
@@ -24,20 +25,33 @@ struct EwArgs {
 };
 
 
-template <int NIN>
+// Load policy is a compile-time choice per launch (a run-time select between a nontemporal and an
+// ordinary load of the same address is folded into one ordinary load by the compiler). Launches
+// whose operands are all read once stream them with nontemporal loads; launches with an operand
+// re-read along a broadcast axis use ordinary loads, so the reuse hits in the caches.
+template <bool REUSE>
+__device__ __forceinline__ f4 load_operand(const float *p) {
+  if constexpr (REUSE) return *reinterpret_cast<const f4 *>(p);
+  else return __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+}
+
+template <bool REUSE, int NIN>
 __device__ __forceinline__ f4 load4(const EwArgs<NIN> &A, int k, int64_t off) {
   if (A.bcast_inner & (1u << k)) return f4(A.in[k][off]);
-  return __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A.in[k] + off));
+  return load_operand<REUSE>(A.in[k] + off);
 }
 
 // Vectorised kernel: innermost axis has stride 1 (output, streamed inputs) or 0 (broadcast
 // inputs) and a multiple-of-4 extent; the other ORANK axes (ORANK < 0: runtime count) are decoded
 // from the unit index with magic division. A workgroup owns kBlock * kEwUnroll consecutive units,
 // so each wave reads and writes whole contiguous 1 KiB runs per operand.
-template <class Body, int ORANK>
+template <class Body, int ORANK, bool REUSE>
 __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
   constexpr int kEwUnroll = Body::kUnroll;
+  // measured: ordinary stores when every operand streams once, nontemporal stores when an operand
+  // is re-read from cache (config 2 chain 6.2 -> 6.6 TB/s; config 3 multiply 5.4 -> 6.9 TB/s)
+  constexpr bool kNtStore = PLAST_EW_NT_STORE < 0 ? REUSE : PLAST_EW_NT_STORE != 0;
   const uint64_t base = uint64_t(blockIdx.x) * (kBlock * kEwUnroll) + threadIdx.x;
   f4 x[kEwUnroll][NIN];
   int64_t oo[kEwUnroll];
@@ -73,7 +87,7 @@ __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Bod
       }
     }
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) x[u][k] = load4(A, k, off[k]);
+    for (int k = 0; k < NIN; ++k) x[u][k] = load4<REUSE>(A, k, off[k]);
     oo[u] = ooff;
   }
   uint64_t idx[kEwUnroll];
@@ -87,7 +101,7 @@ __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Bod
   body.template eval_units<kEwUnroll>(x, idx, valid, r);
 #pragma unroll
   for (int u = 0; u < kEwUnroll; ++u)
-    if (valid[u]) __builtin_nontemporal_store(r[u], reinterpret_cast<f4 *>(A.out + oo[u]));
+    if (valid[u]) store_stream<kNtStore>(r[u], reinterpret_cast<f4 *>(A.out + oo[u]));
 }
 
 // Generic kernel: any strides, one element per lane per step. IDX64 selects 64-bit division for
@@ -190,44 +204,58 @@ __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, 
       for (int c = 0; c < 4; ++c) tile[b * (kTile + kTilePad) + a4 + c] = v[r][c];
     }
   }
-  __syncthreads();
-  // produce: thread t writes float4 (along p) of output rows a = t/16 + 16r, two rows at a time
+  // an unstaged operand constant along q (stride 0 there) has the same float4 on every output row
+  // of the thread: load it once
   const uint32_t b4 = (t & 15) * 4;
+  f4 rowfree[NIN];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    f4 x[2][NIN];
-    uint64_t idx[2] = {0, 0};  // the NEG rule never applies to a strided chain
-    bool valid[2];
+  for (int k = 0; k < NIN; ++k) {
+    rowfree[k] = f4(0.0f);
+    if (!(A.lds_mask >> k & 1u) && A.qst[k] == 0 && A.pst[k] != 0 && p0 + b4 < A.ep)
+      rowfree[k] = load_operand<true>(A.in[k] + base[k] + int64_t(p0 + b4) * A.pst[k]);
+  }
+  __syncthreads();
+  // produce: thread t writes float4 (along p) of output rows a = t/16 + 16r, one row per body
+  // evaluation (measured best: fewer live registers)
 #pragma unroll
-    for (int r2 = 0; r2 < 2; ++r2) {
-      const uint32_t a = (t >> 4) + 16 * (2 * h + r2);
-      valid[r2] = q0 + a < A.eq && p0 + b4 < A.ep;
-      if (!valid[r2]) continue;
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t a = (t >> 4) + 16 * r;
+    f4 x[1][NIN];
+    const uint64_t idx[1] = {0};  // the NEG rule never applies to a strided chain
+    const bool valid[1] = {q0 + a < A.eq && p0 + b4 < A.ep};
+    if (valid[0]) {
 #pragma unroll
       for (int k = 0; k < NIN; ++k) {
         if (A.lds_mask >> k & 1u) {
           const float *tile = lds + A.lds_slot[k] * (kTile * (kTile + kTilePad));
 #pragma unroll
-          for (int c = 0; c < 4; ++c) x[r2][k][c] = tile[(b4 + c) * (kTile + kTilePad) + a];
+          for (int c = 0; c < 4; ++c) x[0][k][c] = tile[(b4 + c) * (kTile + kTilePad) + a];
         } else {
           const float *src =
               A.in[k] + base[k] + int64_t(q0 + a) * A.qst[k] + int64_t(p0 + b4) * A.pst[k];
-          x[r2][k] = A.pst[k] == 0 ? f4(src[0])
-                                   : __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src));
+          // operands not staged through LDS are broadcast along q or p (re-read), or direct
+          if (A.pst[k] == 0) x[0][k] = f4(src[0]);
+          else if (A.qst[k] == 0) x[0][k] = rowfree[k];
+          else x[0][k] = load_operand<true>(src);
         }
       }
     }
-    f4 res[2];
-    body.template eval_units<2>(x, idx, valid, res);
-#pragma unroll
-    for (int r2 = 0; r2 < 2; ++r2) {
-      if (!valid[r2]) continue;
-      const uint32_t a = (t >> 4) + 16 * (2 * h + r2);
-      __builtin_nontemporal_store(
-          res[r2], reinterpret_cast<f4 *>(A.out + base[NIN] + int64_t(q0 + a) * A.qst[NIN] +
-                                          int64_t(p0 + b4)));
-    }
+    f4 res[1];
+    body.template eval_units<1>(x, idx, valid, res);
+    if (valid[0])
+      store_stream<PLAST_TILE_NT_STORE>(res[0], reinterpret_cast<f4 *>(A.out + base[NIN] +
+                                                   int64_t(q0 + a) * A.qst[NIN] + int64_t(p0 + b4)));
   }
+}
+
+// Bit k set when input k of collapsed space `s` has stride 0 on an axis of extent > 1.
+template <int NIN>
+uint32_t reused_mask(const Space &s) {
+  uint32_t m = 0;
+  for (int k = 0; k < NIN; ++k)
+    for (int d = 0; d < s.rank; ++d)
+      if (s.st[k][d] == 0 && s.shape[d] > 1) m |= 1u << k;
+  return m;
 }
 
 // Try the transposed-operand kernel on collapsed space `s`; false when the layout does not fit.
@@ -321,6 +349,7 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
   }
   const int in_ax = s.rank - 1;
   const uint64_t inner = s.shape[in_ax];
+  A.reused = reused_mask<NIN>(s);
 
   // --- vectorised path
   bool vec = (n < (uint64_t(1) << 32) || in_ax == 0) && inner % 4 == 0 && s.st[NIN][in_ax] == 1 && aligned16(out);
@@ -340,11 +369,22 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
     const unsigned grid = ceil_div(A.units, uint64_t(kBlock) * Body::kUnroll);
-    switch (in_ax) {
-    case 0: ew_vec_kernel<Body, 0><<<grid, kBlock, 0, stream()>>>(A, body); break;
-    case 1: ew_vec_kernel<Body, 1><<<grid, kBlock, 0, stream()>>>(A, body); break;
-    case 2: ew_vec_kernel<Body, 2><<<grid, kBlock, 0, stream()>>>(A, body); break;
-    default: ew_vec_kernel<Body, -1><<<grid, kBlock, 0, stream()>>>(A, body); break;
+    // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
+    const bool reuse = (A.reused & ~A.bcast_inner) != 0;
+    if (reuse) {
+      switch (in_ax) {
+      case 0: ew_vec_kernel<Body, 0, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      case 1: ew_vec_kernel<Body, 1, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      case 2: ew_vec_kernel<Body, 2, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      default: ew_vec_kernel<Body, -1, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      }
+    } else {
+      switch (in_ax) {
+      case 0: ew_vec_kernel<Body, 0, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      case 1: ew_vec_kernel<Body, 1, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      case 2: ew_vec_kernel<Body, 2, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      default: ew_vec_kernel<Body, -1, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
+      }
     }
     return true;
   }

@@ -258,7 +258,7 @@ __global__ __launch_bounds__(kBlock) void copy_kernel(f4 *__restrict__ dst,
 #pragma unroll
   for (int k = 0; k < kCopyUnroll; ++k) {
     uint64_t i = base + uint64_t(k) * kBlock;
-    if (i < n4) __builtin_nontemporal_store(v[k], dst + i);
+    if (i < n4) store_stream<PLAST_COPY_NT_STORE>(v[k], dst + i);
   }
 }
 

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__res
       if constexpr (OVERWRITE) r[c] = gv;
       else r[c] = dv[u][c] + gv;
     }
-    __builtin_nontemporal_store(r, d4 + q);
+    store_stream<PLAST_CE_NT_STORE>(r, d4 + q);
   }
 }
 
