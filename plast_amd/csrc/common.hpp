@@ -22,6 +22,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_TAPE_UNROLL
 #define PLAST_TAPE_UNROLL 2  // float4 units per lane, fused-chain interpreter
 #endif
+#ifndef PLAST_TAPE_TILE_ROWS
+#define PLAST_TAPE_TILE_ROWS 2  // fused chains in the transposed-operand tile: rows per evaluation
+#endif
 #ifndef PLAST_ROW_UNROLL
 #define PLAST_ROW_UNROLL 4   // float4 loads in flight per lane, row reductions
 #endif
@@ -43,6 +46,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 #ifndef PLAST_COPY_NT_STORE
 #define PLAST_COPY_NT_STORE 0
+#endif
+#ifndef PLAST_CE_BWD_MODE
+#define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
 #endif
 #ifndef PLAST_CE_BWD_UNROLL
 #define PLAST_CE_BWD_UNROLL 1  // float4 units per lane, cross-entropy backward

@@ -79,6 +79,8 @@ __device__ __forceinline__ float grad_b(float g, float x, float y, bool simd) {
 template <class Derived>
 struct ScalarBody {
   static constexpr int kUnroll = PLAST_EW_UNROLL;  // float4 units per lane
+  static constexpr bool kTileFixed3 = false;       // fixed-role tile kernels for 3 operands
+  static constexpr int kTileRows = 1;              // tile rows per evaluation
   template <int U, int N>
   __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
                                              const bool (&valid)[U], f4 (&acc)[U]) const {
@@ -174,6 +176,8 @@ template <int N, bool TRIG>
 struct TapeBody {
   static constexpr int NIN = N;
   static constexpr int kUnroll = PLAST_TAPE_UNROLL;  // float4 units per lane (keeps the interpreter under 64 VGPRs)
+  static constexpr bool kTileFixed3 = true;
+  static constexpr int kTileRows = PLAST_TAPE_TILE_ROWS;
   PlastFusedTape t;
   uint64_t simd_end;
 

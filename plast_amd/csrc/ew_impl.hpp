@@ -2,6 +2,9 @@
 // units that instantiate it).
 #pragma once
 
+#include <type_traits>
+#include <utility>
+
 #include "ew.hpp"
 
 namespace plast {
@@ -159,12 +162,15 @@ struct TileArgs {
   int64_t qst[NIN + 1], pst[NIN + 1];
   uint32_t eq, ep;                 // extents of q and p
   uint32_t tq, tp;                 // tiles along q and p
+  MagicDiv dtq, dtp;
   uint32_t lds_mask;               // bit k: input k is staged through LDS
   uint32_t lds_slot[NIN];
   uint64_t row_stride_p_index;     // elements per unit of the output's q coordinate in idx terms
 };
 
-template <class Body>
+// DIRECT: whether some operand has role 3 (below); without one, the produce loop issues no global
+// load at all, so nothing in it waits on the memory counter that its stores advance.
+template <class Body, bool DIRECT>
 __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
   extern __shared__ float lds[];
@@ -204,40 +210,66 @@ __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, 
       for (int c = 0; c < 4; ++c) tile[b * (kTile + kTilePad) + a4 + c] = v[r][c];
     }
   }
-  // an unstaged operand constant along q (stride 0 there) has the same float4 on every output row
-  // of the thread: load it once
-  const uint32_t b4 = (t & 15) * 4;
-  f4 rowfree[NIN];
+  // Operand roles, two bits each, held in one SGPR for the produce loop (re-reading them from the
+  // argument block there would wait on the counter that also tracks the LDS reads):
+  // 0 staged through LDS, 1 broadcast along p (one scalar per output row), 2 broadcast along q
+  // (one float4 for all of the thread's rows), 3 direct (float4 along p, read per row).
+  uint32_t roles = 0, slots = 0;
 #pragma unroll
   for (int k = 0; k < NIN; ++k) {
-    rowfree[k] = f4(0.0f);
-    if (!(A.lds_mask >> k & 1u) && A.qst[k] == 0 && A.pst[k] != 0 && p0 + b4 < A.ep)
-      rowfree[k] = load_operand<true>(A.in[k] + base[k] + int64_t(p0 + b4) * A.pst[k]);
+    const uint32_t role = (A.lds_mask >> k & 1u) ? 0u : A.pst[k] == 0 ? 1u : A.qst[k] == 0 ? 2u : 3u;
+    roles |= role << (2 * k);
+    slots |= (A.lds_slot[k] & 3u) << (2 * k);
   }
+  roles = __builtin_amdgcn_readfirstlane(roles);
+  slots = __builtin_amdgcn_readfirstlane(slots);
+  // Roles 1 and 2 are read here, before the barrier and before any store: on this architecture one
+  // memory counter covers loads and stores, so a load waited for after a store also waits for it.
+  const uint32_t b4 = (t & 15) * 4;
+  f4 pre[NIN];
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) {
+    pre[k] = f4(0.0f);
+    const uint32_t role = roles >> (2 * k) & 3u;
+    const float *in = A.in[k] + base[k];
+    if (role == 1u) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t a = (t >> 4) + 16 * r;
+        if (q0 + a < A.eq) pre[k][r] = in[int64_t(q0 + a) * A.qst[k]];
+      }
+    } else if (role == 2u) {
+      if (p0 + b4 < A.ep) pre[k] = load_operand<true>(in + int64_t(p0 + b4) * A.pst[k]);
+    }
+  }
+  // consume every prefetched register on every path here, so no wait for them lands after a store
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) asm volatile("" : "+v"(pre[k]));
   __syncthreads();
   // produce: thread t writes float4 (along p) of output rows a = t/16 + 16r, one row per body
-  // evaluation (measured best: fewer live registers)
+  // evaluation (fewer live registers)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const uint32_t a = (t >> 4) + 16 * r;
     f4 x[1][NIN];
     const uint64_t idx[1] = {0};  // the NEG rule never applies to a strided chain
     const bool valid[1] = {q0 + a < A.eq && p0 + b4 < A.ep};
-    if (valid[0]) {
 #pragma unroll
-      for (int k = 0; k < NIN; ++k) {
-        if (A.lds_mask >> k & 1u) {
-          const float *tile = lds + A.lds_slot[k] * (kTile * (kTile + kTilePad));
+    for (int k = 0; k < NIN; ++k) {
+      const uint32_t role = roles >> (2 * k) & 3u;
+      if (role == 0u) {
+        const float *tile = lds + (slots >> (2 * k) & 3u) * (kTile * (kTile + kTilePad));
 #pragma unroll
-          for (int c = 0; c < 4; ++c) x[0][k][c] = tile[(b4 + c) * (kTile + kTilePad) + a];
-        } else {
-          const float *src =
-              A.in[k] + base[k] + int64_t(q0 + a) * A.qst[k] + int64_t(p0 + b4) * A.pst[k];
-          // operands not staged through LDS are broadcast along q or p (re-read), or direct
-          if (A.pst[k] == 0) x[0][k] = f4(src[0]);
-          else if (A.qst[k] == 0) x[0][k] = rowfree[k];
-          else x[0][k] = load_operand<true>(src);
-        }
+        for (int c = 0; c < 4; ++c) x[0][k][c] = tile[(b4 + c) * (kTile + kTilePad) + a];
+      } else if (role == 1u) {
+        x[0][k] = f4(pre[k][r]);
+      } else if (role == 2u) {
+        x[0][k] = pre[k];
+      } else if (DIRECT && valid[0]) {
+        x[0][k] = load_operand<true>(A.in[k] + base[k] + int64_t(q0 + a) * A.qst[k] +
+                                     int64_t(p0 + b4) * A.pst[k]);
+      } else {
+        x[0][k] = f4(0.0f);
       }
     }
     f4 res[1];
@@ -246,6 +278,170 @@ __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, 
       store_stream<PLAST_TILE_NT_STORE>(res[0], reinterpret_cast<f4 *>(A.out + base[NIN] +
                                                    int64_t(q0 + a) * A.qst[NIN] + int64_t(p0 + b4)));
   }
+}
+
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 (a loop whose index is a constant
+// expression).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+constexpr uint32_t tile_role(uint32_t roles, int k) { return (roles >> (2 * k)) & 3u; }
+
+// Tile kernel with compile-time operand roles (two bits per operand in ROLES, same meaning as
+// above) for spaces whose q and p extents are multiples of the tile (no edge guards), and for the
+// role patterns launch_tile_fixed lists. Every global read of the tile is issued before the
+// barrier, into registers sized for exactly the roles present, from one base address per operand
+// plus a constant row step; the produce loop reads only LDS and registers, so the compiler places
+// no memory-counter wait between the stores of one row and the next.
+template <class Body, uint32_t ROLES>
+__global__ __launch_bounds__(kBlock) void ew_tile_fixed_kernel(TileArgs<Body::NIN> A, Body body) {
+  constexpr int NIN = Body::NIN;
+  extern __shared__ float lds[];
+  const uint32_t bid = blockIdx.x;
+  const uint32_t bq = A.dtp.div(bid);         // blockIdx = (batch * tq + tqi) * tp + tpi
+  const uint32_t tpi = bid - bq * A.tp;
+  const uint32_t bi = A.dtq.div(bq);
+  const uint32_t tqi = bq - bi * A.tq;
+  int64_t base[NIN + 1] = {};
+  uint32_t rem = bi;
+  for (int d = A.nbatch - 1; d >= 0; --d) {
+    const uint32_t nxt = A.bdv[d].div(rem);
+    const int64_t c = int64_t(rem - nxt * A.bdv[d].d);
+    rem = nxt;
+#pragma unroll
+    for (int k = 0; k <= NIN; ++k) base[k] += c * A.bst[k][d];
+  }
+  const int64_t q0 = int64_t(tqi) * kTile, p0 = int64_t(tpi) * kTile;
+  const int t = threadIdx.x;
+  const uint32_t l4 = (t & 15) * 4, r16 = t >> 4;
+
+  // staged (role 0): float4 along q of tile rows p0 + r16 + 16r; role 1: the scalar of each output
+  // row q0 + r16 + 16r; role 2: one float4 along p; role 3: float4 along p of each output row
+  f4 v[NIN][4];
+  static_for<NIN>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr uint32_t role = tile_role(ROLES, k);
+    const float *in = A.in[k] + base[k];
+    if constexpr (role == 0) {
+      const float *src = in + (q0 + l4) * A.qst[k] + (p0 + r16) * A.pst[k];
+      const int64_t step = 16 * A.pst[k];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        v[k][r] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src + r * step));
+    } else if constexpr (role == 1) {
+      const float *src = in + (q0 + r16) * A.qst[k];
+      const int64_t step = 16 * A.qst[k];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[k][r] = f4(src[r * step]);
+    } else if constexpr (role == 2) {
+      v[k][0] = load_operand<true>(in + (p0 + l4) * A.pst[k]);
+    } else {
+      const float *src = in + (q0 + r16) * A.qst[k] + (p0 + l4);
+      const int64_t step = 16 * A.qst[k];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[k][r] = load_operand<true>(src + r * step);
+    }
+  });
+  // staged operands to LDS, in operand order (the host numbers their slots the same way)
+  static_for<NIN>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    if constexpr (tile_role(ROLES, k) == 0) {
+      int slot = 0;
+      for (int j = 0; j < k; ++j) slot += tile_role(ROLES, j) == 0 ? 1 : 0;
+      float *tile = lds + slot * (kTile * (kTile + kTilePad));
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) tile[(r16 + 16 * r) * (kTile + kTilePad) + l4 + c] = v[k][r][c];
+    }
+  });
+  __syncthreads();
+  float *dst = A.out + base[NIN] + (q0 + r16) * A.qst[NIN] + (p0 + l4);
+  const int64_t dstep = 16 * A.qst[NIN];
+  // TR output rows per body evaluation: an interpreted body pays its dispatch once per TR rows
+  constexpr int TR = Body::kTileRows;
+#pragma unroll
+  for (int h = 0; h < 4 / TR; ++h) {
+    f4 x[TR][NIN];
+#pragma unroll
+    for (int u = 0; u < TR; ++u) {
+      const int r = h * TR + u;
+      const uint32_t a = r16 + 16 * r;
+      static_for<NIN>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (tile_role(ROLES, k) == 0) {
+          int slot = 0;
+          for (int j = 0; j < k; ++j) slot += tile_role(ROLES, j) == 0 ? 1 : 0;
+          const float *tile = lds + slot * (kTile * (kTile + kTilePad));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) x[u][k][c] = tile[(l4 + c) * (kTile + kTilePad) + a];
+        } else if constexpr (tile_role(ROLES, k) == 2) {
+          x[u][k] = v[k][0];
+        } else {
+          x[u][k] = v[k][r];
+        }
+      });
+    }
+    uint64_t idx[TR];
+    bool valid[TR];
+#pragma unroll
+    for (int u = 0; u < TR; ++u) {
+      idx[u] = 0;  // the NEG rule never applies to a strided chain
+      valid[u] = true;
+    }
+    f4 res[TR];
+    body.template eval_units<TR>(x, idx, valid, res);
+#pragma unroll
+    for (int u = 0; u < TR; ++u)
+      store_stream<PLAST_TILE_NT_STORE>(res[u], reinterpret_cast<f4 *>(dst + (h * TR + u) * dstep));
+  }
+}
+
+constexpr uint32_t tile_roles(uint32_t r0, uint32_t r1 = 0, uint32_t r2 = 0) {
+  return r0 | r1 << 2 | r2 << 4;
+}
+
+// Launch the fixed-role kernel when `roles` is one of the instantiated patterns.
+template <class Body>
+bool launch_tile_fixed(const TileArgs<Body::NIN> &A, const Body &body, uint32_t roles,
+                       unsigned blocks, size_t lds_bytes) {
+  constexpr int NIN = Body::NIN;
+#define PLAST_TILE_CASE(R)                                                                         \
+  case R:                                                                                          \
+    ew_tile_fixed_kernel<Body, R><<<blocks, kBlock, lds_bytes, stream()>>>(A, body);               \
+    return true;
+  if constexpr (NIN == 1) {
+    switch (roles) { PLAST_TILE_CASE(tile_roles(0)) default: return false; }
+  } else if constexpr (NIN == 2) {
+    switch (roles) {
+      PLAST_TILE_CASE(tile_roles(0, 0))
+      PLAST_TILE_CASE(tile_roles(0, 1))
+      PLAST_TILE_CASE(tile_roles(1, 0))
+      PLAST_TILE_CASE(tile_roles(0, 2))
+      PLAST_TILE_CASE(tile_roles(2, 0))
+      PLAST_TILE_CASE(tile_roles(0, 3))
+      PLAST_TILE_CASE(tile_roles(3, 0))
+    default: return false;
+    }
+  } else if constexpr (NIN == 3 && Body::kTileFixed3) {
+    switch (roles) {
+      PLAST_TILE_CASE(tile_roles(0, 1, 2))
+      PLAST_TILE_CASE(tile_roles(0, 2, 1))
+      PLAST_TILE_CASE(tile_roles(0, 1, 1))
+      PLAST_TILE_CASE(tile_roles(0, 2, 2))
+      PLAST_TILE_CASE(tile_roles(0, 3, 3))
+    default: return false;
+    }
+  } else {
+    return false;
+  }
+#undef PLAST_TILE_CASE
 }
 
 // Bit k set when input k of collapsed space `s` has stride 0 on an axis of extent > 1.
@@ -322,7 +518,19 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
   const uint64_t blocks = batch * A.tq * A.tp;
   if (blocks >= (uint64_t(1) << 31)) return false;
   const size_t lds_bytes = size_t(slots) * kTile * (kTile + kTilePad) * sizeof(float);
-  ew_tile_kernel<Body><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
+  bool direct = false;
+  uint32_t roles = 0;
+  for (int k = 0; k < NIN; ++k) {
+    const uint32_t role = (A.lds_mask >> k & 1u) ? 0u : A.pst[k] == 0 ? 1u : A.qst[k] == 0 ? 2u : 3u;
+    direct = direct || role == 3u;
+    roles |= role << (2 * k);
+  }
+  A.dtq = MagicDiv::make(A.tq);
+  A.dtp = MagicDiv::make(A.tp);
+  const bool full = A.eq % kTile == 0 && A.ep % kTile == 0;
+  if (full && launch_tile_fixed(A, body, roles, unsigned(blocks), lds_bytes)) return true;
+  if (direct) ew_tile_kernel<Body, true><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
+  else ew_tile_kernel<Body, false><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
   return true;
 }
 

@@ -276,6 +276,77 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__res
   }
 }
 
+// Backward, float4 path over the flattened [N, C] gradient: one float4 per lane, its row found by
+// magic division; the per-row constants are cached vector loads shared by the wave.
+template <bool OVERWRITE>
+__global__ __launch_bounds__(kCeBlock) void ce_bwd_flat_kernel(const float *__restrict__ x,
+                                                               const int32_t *__restrict__ lab,
+                                                               const float *__restrict__ stats,
+                                                               const float *__restrict__ dloss,
+                                                               float *dx, MagicDiv dc4,
+                                                               uint32_t units) {
+  const uint32_t q = blockIdx.x * kCeBlock + threadIdx.x;
+  if (q >= units) return;
+  const uint32_t row = dc4.div(q);
+  const uint32_t j4 = q - row * dc4.d;
+  const f4 xv = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(x) + q);
+  f4 dv;
+  if constexpr (!OVERWRITE) dv = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(dx) + q);
+  const float m = stats[2 * uint64_t(row)], l = stats[2 * uint64_t(row) + 1], g = dloss[row];
+  const int32_t y = lab[row];
+  f4 r;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float sm = exp_le0((xv[c] - m) - l);
+    const float oh = int32_t(j4 * 4 + c) == y ? 1.0f : 0.0f;
+    const float gv = g * (sm - oh);
+    if constexpr (OVERWRITE) r[c] = gv;
+    else r[c] = dv[c] + gv;
+  }
+  store_stream<PLAST_CE_NT_STORE>(r, reinterpret_cast<f4 *>(dx) + q);
+}
+
+// Backward, float4 path: one workgroup per row, kBwdUnroll float4 per lane in flight per step.
+template <bool OVERWRITE>
+__global__ __launch_bounds__(kCeBlock) void ce_bwd_row_kernel(const float *__restrict__ x,
+                                                              const int32_t *__restrict__ lab,
+                                                              const float *__restrict__ stats,
+                                                              const float *__restrict__ dloss,
+                                                              float *dx, uint32_t C) {
+  const uint64_t row = blockIdx.x;
+  const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
+  const int32_t y = lab[row];
+  const uint32_t C4 = C / 4;
+  const f4 *x4 = reinterpret_cast<const f4 *>(x + row * C);
+  f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
+  for (uint32_t q0 = threadIdx.x; q0 < C4; q0 += kCeBlock * kBwdUnroll) {
+    f4 xv[kBwdUnroll], dv[kBwdUnroll];
+#pragma unroll
+    for (int u = 0; u < kBwdUnroll; ++u) {
+      const uint32_t q = q0 + uint32_t(u) * kCeBlock;
+      if (q < C4) {
+        xv[u] = __builtin_nontemporal_load(x4 + q);
+        if constexpr (!OVERWRITE) dv[u] = __builtin_nontemporal_load(d4 + q);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBwdUnroll; ++u) {
+      const uint32_t q = q0 + uint32_t(u) * kCeBlock;
+      if (q >= C4) continue;
+      f4 r;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float sm = exp_le0((xv[u][c] - m) - l);
+        const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
+        const float gv = g * (sm - oh);
+        if constexpr (OVERWRITE) r[c] = gv;
+        else r[c] = dv[u][c] + gv;
+      }
+      store_stream<PLAST_CE_NT_STORE>(r, d4 + q);
+    }
+  }
+}
+
 // Backward, any alignment: one element per lane per step.
 template <bool OVERWRITE>
 __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__restrict__ x,
@@ -393,7 +464,18 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
   const float *ps = static_cast<const float *>(st->data);
   const float *pg = static_cast<const float *>(output->grad->data);
   const bool over = params.keepdim == 1;
-  if (vec && over)
+  const uint64_t units = N * uint64_t(C / 4);
+  if (vec && PLAST_CE_BWD_MODE == 1 && units < (uint64_t(1) << 32)) {
+    const MagicDiv dc4 = MagicDiv::make(C / 4);
+    const unsigned g = ceil_div(units, kCeBlock);
+    if (over)
+      ce_bwd_flat_kernel<true><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+    else
+      ce_bwd_flat_kernel<false><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+  } else if (vec && PLAST_CE_BWD_MODE == 2 && N < (uint64_t(1) << 31)) {
+    if (over) ce_bwd_row_kernel<true><<<unsigned(N), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
+    else ce_bwd_row_kernel<false><<<unsigned(N), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
+  } else if (vec && over)
     ce_bwd_vec_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   else if (vec)
     ce_bwd_vec_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
