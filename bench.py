@@ -275,6 +275,52 @@ class C5(Workload):
             forward("sum", [self.G], self.gb, KernelParams(0, 0, 0.0))
 
 
+class Optim(Workload):
+    """Optimizer row: one step of SGD / Adam / AdamW over `count` fp32 parameters totalling 64M
+    elements (gradients ~ N(0, 0.1)), or zero_grad of a 64M gradient. Bytes per element: SGD reads
+    p, g and writes p (12 B); Adam/AdamW read p, g, m, v and write p, m, v (28 B); zero_grad writes
+    4 B."""
+
+    def __init__(self, kind, count=1):
+        self.kind, self.count = kind, count
+        # zero_grad writes only: a 1 GiB gradient, larger than the 256 MB last-level cache
+        self.elems = 1 << 28 if kind == "zero_grad" else 1 << 26
+        self.name = (f"optim_{kind}_{self.elems >> 20}M" if count == 1 else
+                     f"optim_{kind}_{count}x{self.elems // count}")
+        self.bytes_per_call = self.elems * {"sgd": 12, "adam": 28, "adamw": 28, "zero_grad": 4}[kind]
+
+    def setup(self):
+        n = self.elems // self.count
+        self.params = [DeviceTensor((n,), requires_grad=True, zero=False).fill_("normal", 50 + i, 0.0, 1.0)
+                       for i in range(self.count)]
+        for i, t in enumerate(self.params):
+            t.grad.fill_("normal", 900 + i, 0.0, 0.1)
+        self.ptrs, self._keep = abi.tensor_array(*[t.t for t in self.params])
+        if self.kind == "sgd":
+            self.opt = abi.SGD(1e-3)
+        elif self.kind == "adam":
+            self.opt = abi.Adam(1e-3, 0.9, 0.999, 1e-8, 0, None, None, None, None)
+        elif self.kind == "adamw":
+            self.opt = abi.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01, 0, None, None, None, None)
+        if self.kind in ("adam", "adamw"):
+            self.step()  # first step allocates the moments (outside the timed region)
+            lib().plast_hip_synchronize()
+
+    def step(self):
+        L = lib()
+        if self.kind == "zero_grad":
+            for t in self.params:
+                L.zero_grad_hip(C.byref(t.t))
+        else:
+            getattr(L, f"{self.kind}_step_hip")(C.byref(self.opt), self.ptrs, self.count)
+
+    def free(self):
+        if self.kind in ("adam", "adamw"):
+            getattr(lib(), f"plast_hip_{self.kind}_release")(C.byref(self.opt), self.count)
+        for t in self.params:
+            t.free()
+
+
 class Copy(Workload):
     """float4 device copy of 256 MiB: the measured bandwidth ceiling."""
     name = "copy_256MiB"
@@ -300,6 +346,8 @@ def detail_workloads():
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),
         "c4argmax": C4("argmax", 1), "c4csum": C4("sum", 0), "c4cmax": C4("max", 0),
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
+        "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
+        "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
     }
 
 

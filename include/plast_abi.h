@@ -11,6 +11,7 @@
  *   Op, ForwardKernel, BackwardKernel, OP_TYPE   include/core/op.h:5-44
  *   Node          include/core/node.h:5-14
  *   DAG           include/core/graph.h:7-13
+ *   SGD / Adam / AdamW   include/optimizers/{sgd.h:5-7, adam.h:5-15, adamw.h:5-16}
  *
  * tests/test_abi.py compiles a translation unit that includes both this header and the reference
  * headers and static_asserts equal sizeof/offsetof for every field.
@@ -147,6 +148,37 @@ typedef struct DAG {
   bool changed;
   Arena *arena;
 } DAG;
+
+/* Optimizer state, layout-identical to include/optimizers/sgd.h:5-7, adam.h:5-15 and
+ * adamw.h:5-16. `m` and `v` are the per-parameter moment tensors, allocated on the first step. */
+typedef struct SGD {
+  float lr;
+} SGD;
+
+typedef struct Adam {
+  float lr;
+  float beta1;
+  float beta2;
+  float epsilon;
+  int t;
+  Tensor **m;
+  Tensor **v;
+  Arena *data_arena;
+  Arena *optimizer_arena;
+} Adam;
+
+typedef struct AdamW {
+  float lr;
+  float beta1;
+  float beta2;
+  float epsilon;
+  float weight_decay;
+  int t;
+  Tensor **m;
+  Tensor **v;
+  Arena *data_arena;
+  Arena *optimizer_arena;
+} AdamW;
 
 #ifdef __cplusplus
 }

@@ -129,6 +129,32 @@ typedef struct PlastFusedTape {
   PlastTapeIns ins[PLAST_TAPE_MAX_INS];
 } PlastFusedTape;
 
+/* ------------------------------------------------------------------ optimizers --------------- */
+
+/* Parameter updates over `num_parameters` tensors (parameters[i]->data += f(grad, state)),
+ * replacing sgd_step_cuda / adam_step_cuda / adamw_step_cuda / zero_grad_cuda
+ * (include/optimizers/sgd.h:13, adam.h:24, adamw.h:25, zero_grad.h:11; the reference's CUDA Adam
+ * and AdamW are empty: src/optimizers/cuda/adam.cu:72-73, adamw.cu:20-21). Per element they apply
+ * the reference CPU update in its operation order (src/optimizers/cpu/sgd.c:16-28,
+ * adam.c:21-68, adamw.c:19-69); parameters that are NULL or have no grad are skipped; data and
+ * grad are read as flat arrays of numel(param) floats, as the reference does. All parameters of one
+ * call are updated by one kernel launch per group of up to 32 tensors.
+ * Adam/AdamW: `t` is incremented first and the bias-corrected step
+ * lr_t = lr * sqrt(1 - beta2^t) / (1 - beta1^t) is evaluated on the host exactly as the reference
+ * evaluates it (double sqrt, float powf). On the first call, when optimizer->m is NULL, the moment
+ * tensors are allocated by this library (device memory zero-filled, Tensor structs on the host
+ * heap) and stay owned by it until plast_hip_adam_release / plast_hip_adamw_release; a caller
+ * that sets m and v beforehand (for instance from its own device arenas) keeps ownership of them. */
+void sgd_step_hip(SGD *optimizer, Tensor **parameters, int num_parameters);
+void adam_step_hip(Adam *optimizer, Tensor **parameters, int num_parameters);
+void adamw_step_hip(AdamW *optimizer, Tensor **parameters, int num_parameters);
+/* grad[0 .. numel(t->grad)) = 0 (src/optimizers/cpu/zero_grad.c:4-11). */
+void zero_grad_hip(Tensor *t);
+/* Free moment tensors allocated by the first adam_step_hip / adamw_step_hip and reset m, v to
+ * NULL (no effect on caller-provided ones, which the library never owns). */
+void plast_hip_adam_release(Adam *optimizer, int num_parameters);
+void plast_hip_adamw_release(AdamW *optimizer, int num_parameters);
+
 /* ------------------------------------------------------------------ op table ----------------- */
 
 /* GPU slots for every OP_TYPE this backend implements (CPU slots left NULL): the table the

@@ -677,3 +677,98 @@ void oracle_fused_chain2(const float *a, const float *b, const float *c, float *
     out[i] = expf(t);
   }
 }
+
+/* ---------------------------------------------------------------- optimizers -------------------- */
+
+/* src/optimizers/cpu/sgd.c:16-28: data[j] -= lr * grad[j] over numel(param) floats. */
+void oracle_sgd_step(SGD *o, Tensor **params, int n) {
+  if (!o) return;
+  for (int i = 0; i < n; ++i) {
+    Tensor *p = params[i];
+    if (!p || !p->grad) continue;
+    float *d = (float *)p->data;
+    const float *g = (const float *)p->grad->data;
+    for (u64 j = 0; j < o_numel(p); ++j) d[j] -= o->lr * g[j];
+  }
+}
+
+/* Zero-filled contiguous host tensors shaped like each parameter (adam.c:29-46 allocates them
+ * with init(..., zeros) on the first step). */
+static Tensor **o_moments(Tensor **params, int n) {
+  Tensor **m = (Tensor **)calloc((size_t)n, sizeof(Tensor *));
+  for (int i = 0; m && i < n; ++i) {
+    if (!params[i]) continue;
+    Tensor *t = (Tensor *)calloc(1, sizeof(Tensor));
+    u64 cnt = o_numel(params[i]);
+    t->data = calloc(cnt ? cnt : 1, sizeof(float));
+    t->ndim = params[i]->ndim;
+    u64 s = 1;
+    for (u64 d = t->ndim; d-- > 0;) {
+      t->shape[d] = params[i]->shape[d];
+      t->strides[d] = s;
+      s *= t->shape[d];
+    }
+    t->dtype = FLOAT32;
+    t->device = CPU;
+    m[i] = t;
+  }
+  return m;
+}
+
+void oracle_optimizer_release(Tensor **m, Tensor **v, int n) {
+  Tensor **arrs[2] = {m, v};
+  for (int a = 0; a < 2; ++a) {
+    if (!arrs[a]) continue;
+    for (int i = 0; i < n; ++i)
+      if (arrs[a][i]) {
+        free(arrs[a][i]->data);
+        free(arrs[a][i]);
+      }
+    free(arrs[a]);
+  }
+}
+
+/* adam.c:21-68 and adamw.c:19-69 share everything but AdamW's decoupled decay step
+ * (adamw.c:130), which runs first in each element's update. */
+static void o_adam_like(float lr, float b1, float b2, float eps, float wd, int decoupled, int *t,
+                        Tensor ***mp, Tensor ***vp, Tensor **params, int n) {
+  (*t)++;
+  if (!*mp) {
+    *mp = o_moments(params, n);
+    *vp = o_moments(params, n);
+  }
+  /* the reference's expression: float * double sqrt / float, rounded once to float */
+  float lr_t = lr * sqrt(1.0f - powf(b2, *t)) / (1.0f - powf(b1, *t));
+  for (int i = 0; i < n; ++i) {
+    Tensor *p = params[i];
+    if (!p || !p->grad) continue;
+    float *d = (float *)p->data;
+    const float *g = (const float *)p->grad->data;
+    float *m = (float *)(*mp)[i]->data;
+    float *v = (float *)(*vp)[i]->data;
+    for (u64 j = 0; j < o_numel(p); ++j) {
+      if (decoupled) d[j] -= lr * wd * d[j];
+      m[j] = b1 * m[j] + (1.0f - b1) * g[j];
+      v[j] = b2 * v[j] + (1.0f - b2) * g[j] * g[j];
+      d[j] -= lr_t * m[j] / (sqrtf(v[j]) + eps);
+    }
+  }
+}
+
+void oracle_adam_step(Adam *o, Tensor **params, int n) {
+  if (!o) return;
+  o_adam_like(o->lr, o->beta1, o->beta2, o->epsilon, 0.0f, 0, &o->t, &o->m, &o->v, params, n);
+}
+
+void oracle_adamw_step(AdamW *o, Tensor **params, int n) {
+  if (!o) return;
+  o_adam_like(o->lr, o->beta1, o->beta2, o->epsilon, o->weight_decay, 1, &o->t, &o->m, &o->v,
+              params, n);
+}
+
+/* src/optimizers/cpu/zero_grad.c:4-11 */
+void oracle_zero_grad(Tensor *t) {
+  if (!t || !t->grad) return;
+  float *g = (float *)t->grad->data;
+  for (u64 i = 0; i < o_numel(t->grad); ++i) g[i] = 0.0f;
+}

@@ -20,7 +20,9 @@
  *  - softmax cross-entropy: bit-exact against the reference op chain (src/api/loss.c:97-169) run
  *    through oracle/_ref, plus the invariants that softmax rows sum to 1 and gradient rows sum to 0;
  *  - the broadcast backward (reference uses `omp atomic`, so its order is not fixed): fp64 brute
- *    force within the summation bound.
+ *    force within the summation bound;
+ *  - optimizers: bit-exact against the reference's own src/optimizers/cpu sources compiled into
+ *    oracle/_ref, over several steps, plus a float64 restatement of the update within 1e-6.
  * Deliberate deviation: the reference's is_contiguous never inspects strides[0]
  * (src/core/tensor.c:32-42), so a tensor whose leading stride is 0 or padded is read linearly past
  * its storage. The oracle always honours the real strides.
@@ -65,6 +67,15 @@ void oracle_expand_forward(const Tensor **inputs, Tensor *output, KernelParams p
 /* y = exp(-relu(a*b + c)), evaluated as five separately rounded reference ops (MUL, ADD,
  * LEAKY_RELU(0), NEG, EXP), contiguous fp32 of n elements. Config 2's op chain. */
 void oracle_fused_chain2(const float *a, const float *b, const float *c, float *out, u64 n);
+
+/* Optimizers (src/optimizers/cpu/{sgd,adam,adamw,zero_grad}.c): the same per-element statements
+ * in the same order; Adam/AdamW allocate zero-filled host moment tensors on the first step, freed
+ * by oracle_optimizer_release. Pinned bit-exact against the compiled reference (oracle/_ref). */
+void oracle_sgd_step(SGD *o, Tensor **params, int n);
+void oracle_adam_step(Adam *o, Tensor **params, int n);
+void oracle_adamw_step(AdamW *o, Tensor **params, int n);
+void oracle_zero_grad(Tensor *t);
+void oracle_optimizer_release(Tensor **m, Tensor **v, int n);
 
 #ifdef __cplusplus
 }

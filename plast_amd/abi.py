@@ -122,6 +122,24 @@ class FusedTape(C.Structure):
 ArenaAllocFn = C.CFUNCTYPE(C.c_void_p, C.POINTER(Arena), C.c_uint64, C.c_uint64)
 
 
+# Optimizer state (include/optimizers/sgd.h:5-7, adam.h:5-15, adamw.h:5-16)
+class SGD(C.Structure):
+    _fields_ = [("lr", C.c_float)]
+
+
+class Adam(C.Structure):
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("epsilon", C.c_float), ("t", C.c_int), ("m", TensorPP), ("v", TensorPP),
+                ("data_arena", C.POINTER(Arena)), ("optimizer_arena", C.POINTER(Arena))]
+
+
+class AdamW(C.Structure):
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("epsilon", C.c_float), ("weight_decay", C.c_float), ("t", C.c_int),
+                ("m", TensorPP), ("v", TensorPP), ("data_arena", C.POINTER(Arena)),
+                ("optimizer_arena", C.POINTER(Arena))]
+
+
 def params(dim: int = 0, keepdim: int = 0, fval: float = 0.0) -> KernelParams:
     return KernelParams(dim, keepdim, fval)
 

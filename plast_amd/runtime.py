@@ -60,6 +60,12 @@ class Library:
             "plast_hip_copy": ([C.c_void_p, C.c_void_p, C.c_uint64], None),
             "plast_hip_get_op_impl": ([C.c_int], abi.Op),
             "plast_hip_fuse_elementwise_chains": ([C.POINTER(abi.DAG), abi.ArenaAllocFn], C.c_uint32),
+            "sgd_step_hip": ([C.POINTER(abi.SGD), TensorPP, C.c_int], None),
+            "adam_step_hip": ([C.POINTER(abi.Adam), TensorPP, C.c_int], None),
+            "adamw_step_hip": ([C.POINTER(abi.AdamW), TensorPP, C.c_int], None),
+            "zero_grad_hip": ([TensorP], None),
+            "plast_hip_adam_release": ([C.POINTER(abi.Adam), C.c_int], None),
+            "plast_hip_adamw_release": ([C.POINTER(abi.AdamW), C.c_int], None),
             "arena_alloc_hip": ([C.c_uint64], C.c_void_p),
             "arena_free_hip": ([C.c_void_p], None),
             "arena_memset_hip": ([C.c_void_p, C.c_int, C.c_uint64], None),
