@@ -321,6 +321,41 @@ class Optim(Workload):
             t.free()
 
 
+class Pack(Workload):
+    """Pack row: config 3's permuted view, A_base [256,512,512] as permute (0,2,1), gathered into a
+    contiguous buffer (hip_tensor_pack_init; 256 MiB read + 256 MiB written), or copied to pinned
+    host memory in row-major order (plast_hip_tensor_to_host: pack, then a device-to-host copy of
+    256 MiB over the host link; its GB/s counts the 256 MiB delivered)."""
+
+    def __init__(self, part):
+        self.part = part
+        self.name = {"pack": "pack_permuted_256x512x512", "host": "to_host_permuted_256x512x512"}[part]
+        self.elems = 256 * 512 * 512
+        self.bytes_per_call = self.elems * (8 if part == "pack" else 4)
+
+    def setup(self):
+        self.Ab = DeviceTensor((256, 512, 512), zero=False).fill_("normal", 42, 0.0, 1.0)
+        self.Av = DeviceTensor((256, 512, 512), base=self.Ab, strides=(262144, 1, 512), zero=False)
+        self.host = lib().plast_hip_host_alloc(self.elems * 4) if self.part == "host" else None
+
+    def step(self):
+        L = lib()
+        if self.part == "pack":
+            # the released buffer returns to the library's pack pool, so each call reuses it
+            p = abi.HipTensorPack()
+            L.hip_tensor_pack_init(C.byref(p), C.byref(self.Av.t))
+            L.hip_tensor_pack_release(C.byref(p))
+        else:
+            L.plast_hip_tensor_to_host(C.byref(self.Av.t), self.host)
+
+    def free(self):
+        if self.host:
+            lib().plast_hip_host_free(self.host)
+            self.host = None
+        lib().plast_hip_pack_trim()
+        super().free()
+
+
 class Copy(Workload):
     """float4 device copy of 256 MiB: the measured bandwidth ceiling."""
     name = "copy_256MiB"
@@ -348,6 +383,7 @@ def detail_workloads():
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
+        "pack": Pack("pack"), "tohost": Pack("host"),
     }
 
 

@@ -155,6 +155,41 @@ void zero_grad_hip(Tensor *t);
 void plast_hip_adam_release(Adam *optimizer, int num_parameters);
 void plast_hip_adamw_release(AdamW *optimizer, int num_parameters);
 
+/* ------------------------------------------------------------------ pack / host transfer ----- */
+
+/* A contiguous image of a possibly strided tensor, layout-identical to CudaTensorPack
+ * (include/kernels/pack.h:17-20). */
+typedef struct HipTensorPack {
+  void *data;   /* t->data when t is contiguous, else the packed device buffer */
+  void *_d_buf; /* owned device buffer, or NULL */
+} HipTensorPack;
+
+/* Replace cuda_tensor_pack_init / cuda_tensor_pack_release (include/kernels/pack.h:22-23,
+ * src/kernels/cuda/cuda_pack.cu:28-96): alias a contiguous tensor, otherwise allocate
+ * numel * element-size bytes and gather the view into them in row-major order (any dtype, copied
+ * bit for bit). On failure data is NULL. Contiguity checks every stride (the reference's
+ * is_contiguous ignores strides[0]: src/core/tensor.c:32-42). */
+void hip_tensor_pack_init(HipTensorPack *p, const Tensor *t);
+/* Returns an owned buffer to a library pool (at most 8 GiB kept) for the next pack of a similar
+ * size, without waiting: work that reads the pack must be ordered before its release, as work on
+ * the library stream is. */
+void hip_tensor_pack_release(HipTensorPack *p);
+/* Frees every pooled pack buffer (waits for the library stream first). */
+void plast_hip_pack_trim(void);
+
+/* Host transfers of a possibly strided device tensor, the data movement of the bindings' numpy()
+ * and copy_from_numpy (src/python/bindings.cpp:81-151): to_host writes numel(t) elements in
+ * row-major order to `dst` (packing through a library staging buffer when t is strided);
+ * from_host reads numel(t) row-major elements from `src` into t's view (scattering when t is
+ * strided; a destination with a broadcast axis is rejected). Both return 0 on success, -1 on
+ * error, and return after the copy has completed. */
+int plast_hip_tensor_to_host(const Tensor *t, void *dst);
+int plast_hip_tensor_from_host(Tensor *t, const void *src);
+/* Page-locked host memory (hipHostMalloc) for transfer staging: transfers from and to it run at
+ * the host link's rate without an internal bounce. */
+void *plast_hip_host_alloc(u64 bytes);
+void plast_hip_host_free(void *p);
+
 /* ------------------------------------------------------------------ op table ----------------- */
 
 /* GPU slots for every OP_TYPE this backend implements (CPU slots left NULL): the table the

@@ -122,6 +122,11 @@ class FusedTape(C.Structure):
 ArenaAllocFn = C.CFUNCTYPE(C.c_void_p, C.POINTER(Arena), C.c_uint64, C.c_uint64)
 
 
+# Contiguous image of a possibly strided tensor (include/kernels/pack.h:17-20 CudaTensorPack)
+class HipTensorPack(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("_d_buf", C.c_void_p)]
+
+
 # Optimizer state (include/optimizers/sgd.h:5-7, adam.h:5-15, adamw.h:5-16)
 class SGD(C.Structure):
     _fields_ = [("lr", C.c_float)]

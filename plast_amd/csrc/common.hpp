@@ -71,7 +71,8 @@ hipStream_t stream();
 void finish(const char *where);
 bool ensure_init();
 // Device scratch of at least `bytes`, owned by the library and reused across calls. Slot 0 holds
-// the reduction engine's partial summaries; slot 1 an op's own temporaries (tie counts, extremes).
+// the reduction engine's partial summaries; slot 1 an op's own temporaries (tie counts, extremes);
+// slot 2 the staging buffer of host transfers of strided tensors.
 void *workspace(size_t bytes, int slot = 0);
 
 #define PLAST_HIP_TRY(where, expr)                                                                 \

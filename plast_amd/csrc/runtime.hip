@@ -14,7 +14,7 @@ bool g_sync = true;
 hipStream_t g_stream = nullptr;
 int g_err_count = 0;
 char g_err_msg[512] = "";
-constexpr int kSlots = 2;
+constexpr int kSlots = 3;
 void *g_ws[kSlots] = {};
 size_t g_ws_bytes[kSlots] = {};
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;

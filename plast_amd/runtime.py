@@ -66,6 +66,13 @@ class Library:
             "zero_grad_hip": ([TensorP], None),
             "plast_hip_adam_release": ([C.POINTER(abi.Adam), C.c_int], None),
             "plast_hip_adamw_release": ([C.POINTER(abi.AdamW), C.c_int], None),
+            "hip_tensor_pack_init": ([C.POINTER(abi.HipTensorPack), TensorP], None),
+            "hip_tensor_pack_release": ([C.POINTER(abi.HipTensorPack)], None),
+            "plast_hip_tensor_to_host": ([TensorP, C.c_void_p], C.c_int),
+            "plast_hip_tensor_from_host": ([TensorP, C.c_void_p], C.c_int),
+            "plast_hip_pack_trim": ([], None),
+            "plast_hip_host_alloc": ([C.c_uint64], C.c_void_p),
+            "plast_hip_host_free": ([C.c_void_p], None),
             "arena_alloc_hip": ([C.c_uint64], C.c_void_p),
             "arena_free_hip": ([C.c_void_p], None),
             "arena_memset_hip": ([C.c_void_p, C.c_int, C.c_uint64], None),
