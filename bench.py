@@ -356,6 +356,35 @@ class Pack(Workload):
         super().free()
 
 
+class Epilogue(Workload):
+    """Matmul-epilogue row on a [16384, 4096] output: the leaky-relu gradient modulation
+    dc = dout * (out > 0 ? 1 : alpha) (reads dout, out; writes dc: 12 B/element) and the bias
+    gradient column sum of dc into [4096] (4 B/element + 16 KiB)."""
+
+    def __init__(self, part):
+        self.part = part
+        self.name = {"mod": "epilogue_relu_grad_modulate_16384x4096",
+                     "bias": "epilogue_bias_grad_16384x4096"}[part]
+        self.M, self.N = 16384, 4096
+        self.elems = self.M * self.N
+        self.bytes_per_call = self.elems * 12 if part == "mod" else self.elems * 4 + self.N * 4
+
+    def setup(self):
+        M, N = self.M, self.N
+        self.dout = DeviceTensor((M, N), zero=False).fill_("normal", 60, 0.0, 1.0)
+        self.out = DeviceTensor((M, N), zero=False).fill_("normal", 61, 0.0, 1.0)
+        self.dc = DeviceTensor((M, N), zero=False).fill_("normal", 62, 0.0, 1.0)
+        self.db = DeviceTensor((N,), zero=False)
+
+    def step(self):
+        L = lib()
+        if self.part == "mod":
+            L.launch_relu_grad_modulate_hip(self.dout.ptr, self.out.ptr, self.dc.ptr, self.elems,
+                                            0.01, 0, 0)
+        else:
+            L.bias_grad_reduce_hip(self.dc.ptr, self.db.ptr, self.elems, self.N)
+
+
 class Copy(Workload):
     """float4 device copy of 256 MiB: the measured bandwidth ceiling."""
     name = "copy_256MiB"
@@ -384,6 +413,7 @@ def detail_workloads():
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),
+        "epimod": Epilogue("mod"), "epibias": Epilogue("bias"),
     }
 
 

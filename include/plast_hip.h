@@ -155,6 +155,19 @@ void zero_grad_hip(Tensor *t);
 void plast_hip_adam_release(Adam *optimizer, int num_parameters);
 void plast_hip_adamw_release(AdamW *optimizer, int num_parameters);
 
+/* ------------------------------------------------------------------ matmul epilogue pieces ---- */
+
+/* dc[i] = dout[i] * (out_data[i] > 0 ? 1 : alpha) over num_elements contiguous floats: replaces
+ * launch_relu_grad_modulate_cuda (include/kernels/matmul.h:43, src/kernels/cuda/
+ * matmul_relu.cu:138-151; CPU fused_ops.c:105-111). grid_size and block_size are accepted for
+ * signature compatibility and ignored. */
+void launch_relu_grad_modulate_hip(const float *dout, const float *out_data, float *dc,
+                                   u64 num_elements, float alpha, int grid_size, int block_size);
+/* dbias[c] = sum over rows of dc_mod[row * cols + c] (dbias overwritten), num_elements a multiple
+ * of cols: the bias-gradient column sum of matmul_bias_relu's backward (src/kernels/cuda/
+ * matmul_bias_relu.cu:143-151, 215-220; CPU fused_ops.c:294-304), deterministic (no atomics). */
+void bias_grad_reduce_hip(const float *dc_mod, float *dbias, u64 num_elements, u64 cols);
+
 /* ------------------------------------------------------------------ pack / host transfer ----- */
 
 /* A contiguous image of a possibly strided tensor, layout-identical to CudaTensorPack

@@ -772,3 +772,16 @@ void oracle_zero_grad(Tensor *t) {
   float *g = (float *)t->grad->data;
   for (u64 i = 0; i < o_numel(t->grad); ++i) g[i] = 0.0f;
 }
+
+/* ---------------------------------------------------------------- matmul epilogue pieces -------- */
+
+/* fused_ops.c:19-21, 105-111: dc[i] = dout[i] * (out[i] > 0 ? 1 : alpha). */
+void oracle_relu_grad_modulate(const float *dout, const float *out, float *dc, u64 n, float alpha) {
+  for (u64 i = 0; i < n; ++i) dc[i] = dout[i] * (out[i] > 0.0f ? 1.0f : alpha);
+}
+
+/* fused_ops.c:294-304: dbias zeroed, then rows added in index order. */
+void oracle_bias_grad_reduce(const float *dc, float *dbias, u64 n, u64 cols) {
+  for (u64 c = 0; c < cols; ++c) dbias[c] = 0.0f;
+  for (u64 i = 0; i < n; ++i) dbias[i % cols] += dc[i];
+}

@@ -77,6 +77,11 @@ void oracle_adamw_step(AdamW *o, Tensor **params, int n);
 void oracle_zero_grad(Tensor *t);
 void oracle_optimizer_release(Tensor **m, Tensor **v, int n);
 
+/* The matmul epilogues' elementwise pieces (src/kernels/cpu/fused_ops.c:105-111, 294-304), pinned
+ * through the reference's exported matmul_bias_relu_cpu_backward with an identity weight. */
+void oracle_relu_grad_modulate(const float *dout, const float *out, float *dc, u64 n, float alpha);
+void oracle_bias_grad_reduce(const float *dc, float *dbias, u64 n, u64 cols);
+
 #ifdef __cplusplus
 }
 #endif

@@ -151,6 +151,16 @@ struct BinGradBBody : ScalarBody<BinGradBBody<OP>> {
   }
 };
 
+// operands: dout, out  ->  dout * (out > 0 ? 1 : alpha): the leaky-relu gradient modulation of the
+// fused matmul epilogues (src/kernels/cpu/fused_ops.c:19-21, 105-111)
+struct ReluGradBody : ScalarBody<ReluGradBody> {
+  static constexpr int NIN = 2;
+  float alpha;
+  __device__ __forceinline__ float eval(const float *v, uint64_t) const {
+    return v[0] * (v[1] > 0.0f ? 1.0f : alpha);
+  }
+};
+
 // operands: da, g  ->  da + g  (reshape backward, sum backward broadcast, transpose backward)
 struct AccumBody : ScalarBody<AccumBody> {
   static constexpr int NIN = 2;

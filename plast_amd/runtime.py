@@ -71,6 +71,9 @@ class Library:
             "plast_hip_tensor_to_host": ([TensorP, C.c_void_p], C.c_int),
             "plast_hip_tensor_from_host": ([TensorP, C.c_void_p], C.c_int),
             "plast_hip_pack_trim": ([], None),
+            "launch_relu_grad_modulate_hip": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
+                                               C.c_float, C.c_int, C.c_int], None),
+            "bias_grad_reduce_hip": ([C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64], None),
             "plast_hip_host_alloc": ([C.c_uint64], C.c_void_p),
             "plast_hip_host_free": ([C.c_void_p], None),
             "arena_alloc_hip": ([C.c_uint64], C.c_void_p),
