@@ -29,6 +29,10 @@ class Graph:
         n = abi.Node()
         arr = (abi.TensorP * len(inputs))(*[C.pointer(t.t) for t in inputs])
         self._keep.append(arr)
+        # the nodes point into these tensors' structs and device memory: keep the owners alive
+        # as long as the graph (a collected DeviceTensor frees its buffer)
+        self._keep.extend(inputs)
+        self._keep.append(output)
         n.inputs = C.cast(arr, abi.TensorPP)
         n.output = C.pointer(output.t)
         n.op = L.plast_hip_get_op_impl(abi.OP[op.upper()])
