@@ -16,11 +16,39 @@ constexpr int kMaxRank = PLAST_MAX_NDIM;
 constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 wave64s)
 
 // Launch-shape knobs, measured on MI355X (overridable with -D for sweeps).
+// Vectorised elementwise kernel, per kind of launch: fixed bodies whose operands all stream once
+// (EW), fixed bodies with an operand re-read along a broadcast axis (EWR), fused-chain tapes (TAPE).
+// BLOCK: threads per workgroup; UNROLL: float4 units per lane; XCD 1: consecutive workgroup ranges
+// are mapped onto one XCD each. Measured on MI355X over 64M-element launches: streaming bodies
+// 6.56 -> 7.03-7.15 TB/s with one unit per lane and the XCD mapping (256/4/0 before); the
+// broadcast multiply of config 3 6.91 -> 7.02 TB/s at 512/2 (the XCD mapping costs it 10%); the
+// tape interpreter is fastest at 256/2 without the mapping (one unit per lane: -10 to -15%).
+#ifndef PLAST_EW_BLOCK
+#define PLAST_EW_BLOCK 256
+#endif
 #ifndef PLAST_EW_UNROLL
-#define PLAST_EW_UNROLL 4    // float4 units per lane, fixed elementwise bodies
+#define PLAST_EW_UNROLL 1
+#endif
+#ifndef PLAST_EW_XCD
+#define PLAST_EW_XCD 1
+#endif
+#ifndef PLAST_EWR_BLOCK
+#define PLAST_EWR_BLOCK 512
+#endif
+#ifndef PLAST_EWR_UNROLL
+#define PLAST_EWR_UNROLL 2
+#endif
+#ifndef PLAST_EWR_XCD
+#define PLAST_EWR_XCD 0
+#endif
+#ifndef PLAST_TAPE_BLOCK
+#define PLAST_TAPE_BLOCK 256
 #endif
 #ifndef PLAST_TAPE_UNROLL
-#define PLAST_TAPE_UNROLL 2  // float4 units per lane, fused-chain interpreter
+#define PLAST_TAPE_UNROLL 2
+#endif
+#ifndef PLAST_TAPE_XCD
+#define PLAST_TAPE_XCD 0
 #endif
 #ifndef PLAST_TAPE_TILE_ROWS
 #define PLAST_TAPE_TILE_ROWS 2  // fused chains in the transposed-operand tile: rows per evaluation

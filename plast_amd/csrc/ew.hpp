@@ -78,7 +78,7 @@ __device__ __forceinline__ float grad_b(float g, float x, float y, bool simd) {
 
 template <class Derived>
 struct ScalarBody {
-  static constexpr int kUnroll = PLAST_EW_UNROLL;  // float4 units per lane
+  static constexpr bool kTape = false;             // selects the vectorised launch shape
   static constexpr bool kTileFixed3 = false;       // fixed-role tile kernels for 3 operands
   static constexpr int kTileRows = 1;              // tile rows per evaluation
   template <int U, int N>
@@ -185,7 +185,7 @@ struct AccumDivBody : ScalarBody<AccumDivBody> {
 template <int N, bool TRIG>
 struct TapeBody {
   static constexpr int NIN = N;
-  static constexpr int kUnroll = PLAST_TAPE_UNROLL;  // float4 units per lane (keeps the interpreter under 64 VGPRs)
+  static constexpr bool kTape = true;
   static constexpr bool kTileFixed3 = true;
   static constexpr int kTileRows = PLAST_TAPE_TILE_ROWS;
   PlastFusedTape t;

@@ -46,21 +46,36 @@ __device__ __forceinline__ f4 load4(const EwArgs<NIN> &A, int k, int64_t off) {
 
 // Vectorised kernel: innermost axis has stride 1 (output, streamed inputs) or 0 (broadcast
 // inputs) and a multiple-of-4 extent; the other ORANK axes (ORANK < 0: runtime count) are decoded
-// from the unit index with magic division. A workgroup owns kBlock * kEwUnroll consecutive units,
+// from the unit index with magic division. A workgroup owns kEwBlock * kEwUnroll consecutive units,
 // so each wave reads and writes whole contiguous 1 KiB runs per operand.
+template <class Body, bool REUSE>
+struct VecLaunch {
+  static constexpr int block = Body::kTape ? PLAST_TAPE_BLOCK : REUSE ? PLAST_EWR_BLOCK : PLAST_EW_BLOCK;
+  static constexpr int unroll = Body::kTape ? PLAST_TAPE_UNROLL : REUSE ? PLAST_EWR_UNROLL : PLAST_EW_UNROLL;
+  static constexpr bool xcd = (Body::kTape ? PLAST_TAPE_XCD : REUSE ? PLAST_EWR_XCD : PLAST_EW_XCD) != 0;
+};
+
 template <class Body, int ORANK, bool REUSE>
-__global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Body body) {
+__global__ __launch_bounds__((VecLaunch<Body, REUSE>::block)) void ew_vec_kernel(EwArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
-  constexpr int kEwUnroll = Body::kUnroll;
+  constexpr int kEwBlock = VecLaunch<Body, REUSE>::block;
+  constexpr int kEwUnroll = VecLaunch<Body, REUSE>::unroll;
   // measured: ordinary stores when every operand streams once, nontemporal stores when an operand
   // is re-read from cache (config 2 chain 6.2 -> 6.6 TB/s; config 3 multiply 5.4 -> 6.9 TB/s)
   constexpr bool kNtStore = PLAST_EW_NT_STORE < 0 ? REUSE : PLAST_EW_NT_STORE != 0;
-  const uint64_t base = uint64_t(blockIdx.x) * (kBlock * kEwUnroll) + threadIdx.x;
+  uint32_t bid = blockIdx.x;
+  if constexpr (VecLaunch<Body, REUSE>::xcd) {
+    // workgroups are dispatched round-robin over the 8 XCDs; renumber so XCD x owns the x-th
+    // contiguous range of the first 8 * (grid / 8) workgroups (a permutation of them)
+    const uint32_t per = gridDim.x / 8;
+    if (bid < per * 8) bid = (bid % 8) * per + bid / 8;
+  }
+  const uint64_t base = uint64_t(bid) * (kEwBlock * kEwUnroll) + threadIdx.x;
   f4 x[kEwUnroll][NIN];
   int64_t oo[kEwUnroll];
 #pragma unroll
   for (int u = 0; u < kEwUnroll; ++u) {
-    const uint64_t q = base + uint64_t(u) * kBlock;
+    const uint64_t q = base + uint64_t(u) * kEwBlock;
     if (q >= A.units) continue;
     int64_t off[NIN];
     int64_t ooff;
@@ -97,8 +112,8 @@ __global__ __launch_bounds__(kBlock) void ew_vec_kernel(EwArgs<Body::NIN> A, Bod
   bool valid[kEwUnroll];
 #pragma unroll
   for (int u = 0; u < kEwUnroll; ++u) {
-    idx[u] = (base + uint64_t(u) * kBlock) * 4;
-    valid[u] = base + uint64_t(u) * kBlock < A.units;
+    idx[u] = (base + uint64_t(u) * kEwBlock) * 4;
+    valid[u] = base + uint64_t(u) * kEwBlock < A.units;
   }
   f4 r[kEwUnroll];
   body.template eval_units<kEwUnroll>(x, idx, valid, r);
@@ -536,6 +551,18 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
 
 // ------------------------------------------------------------------------- host dispatch
 
+template <class Body, bool REUSE>
+void launch_vec(const EwArgs<Body::NIN> &A, const Body &body, int in_ax) {
+  using L = VecLaunch<Body, REUSE>;
+  const unsigned grid = unsigned(ceil_div(A.units, uint64_t(L::block) * L::unroll));
+  switch (in_ax) {
+  case 0: ew_vec_kernel<Body, 0, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
+  case 1: ew_vec_kernel<Body, 1, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
+  case 2: ew_vec_kernel<Body, 2, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
+  default: ew_vec_kernel<Body, -1, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
+  }
+}
+
 template <class Body>
 bool launch_elementwise(const Body &body, const void *const *in, void *out, Space s,
                         const char *where) {
@@ -576,24 +603,9 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.units = n / 4;
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
-    const unsigned grid = ceil_div(A.units, uint64_t(kBlock) * Body::kUnroll);
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
-    const bool reuse = (A.reused & ~A.bcast_inner) != 0;
-    if (reuse) {
-      switch (in_ax) {
-      case 0: ew_vec_kernel<Body, 0, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      case 1: ew_vec_kernel<Body, 1, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      case 2: ew_vec_kernel<Body, 2, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      default: ew_vec_kernel<Body, -1, true><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      }
-    } else {
-      switch (in_ax) {
-      case 0: ew_vec_kernel<Body, 0, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      case 1: ew_vec_kernel<Body, 1, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      case 2: ew_vec_kernel<Body, 2, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      default: ew_vec_kernel<Body, -1, false><<<grid, kBlock, 0, stream()>>>(A, body); break;
-      }
-    }
+    if ((A.reused & ~A.bcast_inner) != 0) launch_vec<Body, true>(A, body, in_ax);
+    else launch_vec<Body, false>(A, body, in_ax);
     return true;
   }
 
