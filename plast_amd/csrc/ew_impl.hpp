@@ -63,13 +63,7 @@ __global__ __launch_bounds__((VecLaunch<Body, REUSE>::block)) void ew_vec_kernel
   // measured: ordinary stores when every operand streams once, nontemporal stores when an operand
   // is re-read from cache (config 2 chain 6.2 -> 6.6 TB/s; config 3 multiply 5.4 -> 6.9 TB/s)
   constexpr bool kNtStore = PLAST_EW_NT_STORE < 0 ? REUSE : PLAST_EW_NT_STORE != 0;
-  uint32_t bid = blockIdx.x;
-  if constexpr (VecLaunch<Body, REUSE>::xcd) {
-    // workgroups are dispatched round-robin over the 8 XCDs; renumber so XCD x owns the x-th
-    // contiguous range of the first 8 * (grid / 8) workgroups (a permutation of them)
-    const uint32_t per = gridDim.x / 8;
-    if (bid < per * 8) bid = (bid % 8) * per + bid / 8;
-  }
+  const uint32_t bid = VecLaunch<Body, REUSE>::xcd ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint64_t base = uint64_t(bid) * (kEwBlock * kEwUnroll) + threadIdx.x;
   f4 x[kEwUnroll][NIN];
   int64_t oo[kEwUnroll];
@@ -531,7 +525,7 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
   A.tq = ceil_div(A.eq, kTile);
   A.tp = ceil_div(A.ep, kTile);
   const uint64_t blocks = batch * A.tq * A.tp;
-  if (blocks >= (uint64_t(1) << 31)) return false;
+  if (blocks > max_blocks(kBlock)) return false;
   const size_t lds_bytes = size_t(slots) * kTile * (kTile + kTilePad) * sizeof(float);
   bool direct = false;
   uint32_t roles = 0;
@@ -551,16 +545,20 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
 
 // ------------------------------------------------------------------------- host dispatch
 
+// Returns false (launching nothing) when the grid would exceed the dispatch limit.
 template <class Body, bool REUSE>
-void launch_vec(const EwArgs<Body::NIN> &A, const Body &body, int in_ax) {
+bool launch_vec(const EwArgs<Body::NIN> &A, const Body &body, int in_ax) {
   using L = VecLaunch<Body, REUSE>;
-  const unsigned grid = unsigned(ceil_div(A.units, uint64_t(L::block) * L::unroll));
+  const uint64_t blocks = (A.units + uint64_t(L::block) * L::unroll - 1) / (uint64_t(L::block) * L::unroll);
+  if (blocks > max_blocks(L::block)) return false;
+  const unsigned grid = unsigned(blocks);
   switch (in_ax) {
   case 0: ew_vec_kernel<Body, 0, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
   case 1: ew_vec_kernel<Body, 1, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
   case 2: ew_vec_kernel<Body, 2, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
   default: ew_vec_kernel<Body, -1, REUSE><<<grid, L::block, 0, stream()>>>(A, body); break;
   }
+  return true;
 }
 
 template <class Body>
@@ -604,9 +602,9 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
-    if ((A.reused & ~A.bcast_inner) != 0) launch_vec<Body, true>(A, body, in_ax);
-    else launch_vec<Body, false>(A, body, in_ax);
-    return true;
+    const bool done = (A.reused & ~A.bcast_inner) != 0 ? launch_vec<Body, true>(A, body, in_ax)
+                                                       : launch_vec<Body, false>(A, body, in_ax);
+    if (done) return true;
   }
 
   // --- transposed-operand path

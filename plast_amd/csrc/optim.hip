@@ -52,7 +52,9 @@ __device__ __forceinline__ void update(const OptArgs &A, float &p, float g, floa
 // three written) run fastest with nontemporal loads and stores (64M parameters: 5.6 -> 5.85
 // TB/s), SGD (two read, one written) with ordinary ones (7.2 vs 6.6 TB/s).
 template <Opt OPT>
-constexpr bool kOptNt = OPT != Opt::Sgd;
+constexpr bool kOptNtLoad = OPT != Opt::Sgd && PLAST_ADAM_NT_LOAD != 0;
+template <Opt OPT>
+constexpr bool kOptNtStore = OPT != Opt::Sgd && PLAST_ADAM_NT_STORE != 0;
 
 template <bool NT>
 __device__ __forceinline__ f4 ld(const float *p) {
@@ -63,7 +65,7 @@ __device__ __forceinline__ f4 ld(const float *p) {
 template <Opt OPT>
 __global__ __launch_bounds__(kBlock) void opt_kernel(OptArgs A) {
   constexpr bool kMoments = OPT != Opt::Sgd;
-  const uint32_t b = blockIdx.x;
+  const uint32_t b = PLAST_OPT_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   int i = 0;
   while (i + 1 < A.count && b >= A.first_block[i + 1]) ++i;  // uniform
   const uint64_t n = A.n[i];
@@ -77,12 +79,12 @@ __global__ __launch_bounds__(kBlock) void opt_kernel(OptArgs A) {
     const uint64_t e = (unit0 + uint64_t(u) * kBlock) * 4;
     if (e >= n) continue;
     if (e + 4 <= n && (A.vec_mask >> i & 1u)) {
-      f4 p = ld<kOptNt<OPT>>(P + e);
+      f4 p = ld<kOptNtLoad<OPT>>(P + e);
       const f4 g = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(G + e));
       f4 m = f4(0.0f), v = f4(0.0f);
       if constexpr (kMoments) {
-        m = ld<kOptNt<OPT>>(M + e);
-        v = ld<kOptNt<OPT>>(V + e);
+        m = ld<kOptNtLoad<OPT>>(M + e);
+        v = ld<kOptNtLoad<OPT>>(V + e);
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -92,10 +94,10 @@ __global__ __launch_bounds__(kBlock) void opt_kernel(OptArgs A) {
         m[c] = mc;
         v[c] = vc;
       }
-      store_stream<kOptNt<OPT>>(p, reinterpret_cast<f4 *>(P + e));
+      store_stream<kOptNtStore<OPT>>(p, reinterpret_cast<f4 *>(P + e));
       if constexpr (kMoments) {
-        store_stream<kOptNt<OPT>>(m, reinterpret_cast<f4 *>(M + e));
-        store_stream<kOptNt<OPT>>(v, reinterpret_cast<f4 *>(V + e));
+        store_stream<kOptNtStore<OPT>>(m, reinterpret_cast<f4 *>(M + e));
+        store_stream<kOptNtStore<OPT>>(v, reinterpret_cast<f4 *>(V + e));
       }
     } else {
       const uint64_t end = e + 4 < n ? e + 4 : n;
@@ -141,28 +143,30 @@ void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int c
       continue;
     }
     const uint64_t n = numel(t);
-    if (n == 0) continue;
-    const uint64_t units = (n + 3) / 4;
-    const uint64_t need = (units + kBlock * kOptUnroll - 1) / (kBlock * kOptUnroll);
-    if (need >= (uint64_t(1) << 31) - blocks) {
-      flush();
-      if (need >= (uint64_t(1) << 31)) {
-        report_error(where, "parameter %d is too large for one launch", k);
-        continue;
-      }
+    float *P = static_cast<float *>(t->data);
+    const float *G = static_cast<const float *>(t->grad->data);
+    float *M = m ? static_cast<float *>(m[k]->data) : nullptr;
+    float *V = v ? static_cast<float *>(v[k]->data) : nullptr;
+    bool aligned = aligned16(P) && aligned16(G);
+    if (m) aligned = aligned && aligned16(M) && aligned16(V);
+    // a tensor longer than one launch's grid allows is updated as several entries
+    const uint64_t per_block = uint64_t(kBlock) * kOptUnroll * 4;
+    const uint64_t max_piece = max_blocks(kBlock) / 2 * per_block;
+    for (uint64_t off = 0; off < n; off += max_piece) {
+      const uint64_t len = n - off < max_piece ? n - off : max_piece;
+      const uint64_t need = (len + per_block - 1) / per_block;
+      if (need > max_blocks(kBlock) - blocks) flush();
+      const int i = A.count;
+      A.p[i] = P + off;
+      A.g[i] = G + off;
+      A.m[i] = M ? M + off : nullptr;
+      A.v[i] = V ? V + off : nullptr;
+      A.n[i] = len;
+      A.first_block[i] = blocks;
+      if (aligned) A.vec_mask |= 1u << i;
+      blocks += uint32_t(need);
+      if (++A.count == kGroup) flush();
     }
-    const int i = A.count;
-    A.p[i] = static_cast<float *>(t->data);
-    A.g[i] = static_cast<const float *>(t->grad->data);
-    A.m[i] = m ? static_cast<float *>(m[k]->data) : nullptr;
-    A.v[i] = v ? static_cast<float *>(v[k]->data) : nullptr;
-    A.n[i] = n;
-    A.first_block[i] = blocks;
-    bool aligned = aligned16(A.p[i]) && aligned16(A.g[i]);
-    if (m) aligned = aligned && aligned16(A.m[i]) && aligned16(A.v[i]);
-    if (aligned) A.vec_mask |= 1u << i;
-    blocks += uint32_t(need);
-    if (++A.count == kGroup) flush();
   }
   flush();
 }

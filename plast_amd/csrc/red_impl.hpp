@@ -606,7 +606,8 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
     G.len = 0;
     G.post = int(post);
     G.divisor = divisor;
-    red_generic_kernel<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(G, prod);
+    const uint64_t gb = (nout + kBlock - 1) / kBlock;
+    red_generic_kernel<Prod, Comb><<<unsigned(gb < 65536 ? gb : 65536), kBlock, 0, stream()>>>(G, prod);
     return true;
   }
   // collapse() never merges a reduced axis with a kept one: the target's stride is 0 on one and
@@ -628,7 +629,10 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
   const bool small_idx = s.numel() < (uint64_t(1) << 32) && nout < (uint64_t(1) << 32);
 
   // ---- rows: single reduced axis, innermost, unit stride for streamed operands
-  if (!empty_space && small_idx && nred == 1 && red_ax == r - 1) {
+  // one wave per row (segment): the grid is rows * segs / 4 workgroups (rows < 2^32 segments
+  // are only split when there are fewer than 4096 rows)
+  if (!empty_space && small_idx && nred == 1 && red_ax == r - 1 &&
+      nout <= max_blocks(kBlock) * (kBlock / 64)) {
     RedArgs<NIN> A;
     memset(&A, 0, sizeof A);
     for (int k = 0; k < NIN; ++k) A.in[k] = static_cast<const float *>(in[k]);
@@ -750,7 +754,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
     A.seglen = seglen;
     A.post = int(post);
     A.divisor = divisor;
-    if (base_blocks < (uint64_t(1) << 31)) {
+    if (base_blocks <= max_blocks(kBlock)) {
       if (chunks > 1) {
         A.part = workspace(sizeof(Part) * nout * chunks);
         if (!A.part) return false;

