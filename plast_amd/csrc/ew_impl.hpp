@@ -183,7 +183,7 @@ template <class Body, bool DIRECT>
 __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
   extern __shared__ float lds[];
-  uint32_t bid = blockIdx.x;
+  uint32_t bid = PLAST_TILE_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint32_t tpi = bid % A.tp;
   bid /= A.tp;
   const uint32_t tqi = bid % A.tq;
@@ -312,7 +312,7 @@ template <class Body, uint32_t ROLES>
 __global__ __launch_bounds__(kBlock) void ew_tile_fixed_kernel(TileArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
   extern __shared__ float lds[];
-  const uint32_t bid = blockIdx.x;
+  const uint32_t bid = PLAST_TILE_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint32_t bq = A.dtp.div(bid);         // blockIdx = (batch * tq + tqi) * tp + tpi
   const uint32_t tpi = bid - bq * A.tp;
   const uint32_t bi = A.dtq.div(bq);

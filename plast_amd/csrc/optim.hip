@@ -62,10 +62,11 @@ __device__ __forceinline__ f4 ld(const float *p) {
   else return *reinterpret_cast<const f4 *>(p);
 }
 
-template <Opt OPT>
+// XCD: XCD-contiguous workgroup numbering (used for launches holding one tensor entry).
+template <Opt OPT, bool XCD>
 __global__ __launch_bounds__(kBlock) void opt_kernel(OptArgs A) {
   constexpr bool kMoments = OPT != Opt::Sgd;
-  const uint32_t b = PLAST_OPT_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint32_t b = XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   int i = 0;
   while (i + 1 < A.count && b >= A.first_block[i + 1]) ++i;  // uniform
   const uint64_t n = A.n[i];
@@ -130,7 +131,8 @@ void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int c
   auto flush = [&]() {
     if (A.count == 0) return;
     A.first_block[A.count] = blocks;
-    opt_kernel<OPT><<<blocks, kBlock, 0, stream()>>>(A);
+    if (PLAST_OPT_XCD && A.count == 1) opt_kernel<OPT, true><<<blocks, kBlock, 0, stream()>>>(A);
+    else opt_kernel<OPT, false><<<blocks, kBlock, 0, stream()>>>(A);
     A.count = 0;
     A.vec_mask = 0;
     blocks = 0;

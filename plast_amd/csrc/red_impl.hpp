@@ -253,7 +253,8 @@ __global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, 
   constexpr int NIN = Prod::NIN;
   using Part = typename Comb::Part;
   const int lane = threadIdx.x & 63;
-  const uint64_t task = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  const uint32_t bx = PLAST_RED_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint64_t task = uint64_t(bx) * (kBlock / 64) + (threadIdx.x >> 6);
   if (task >= A.rows * A.segs) return;  // whole wave exits together
   const uint32_t row = uint32_t(task / A.segs);
   const uint32_t seg = uint32_t(task - uint64_t(row) * A.segs);
@@ -359,14 +360,35 @@ __global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, 
 }
 
 // Combine the segments of each row in index order.
+// Merge segs partials part[0], part[stride], ... in index order. The loads of a batch are issued
+// before its merges: the partials come from L2 or HBM, and a serial load-merge chain would pay
+// that latency once per partial (a [16384, 4096] column sum split in 64 chunks spent most of
+// its time in that chain).
+template <class Comb>
+__device__ __forceinline__ typename Comb::Part merge_in_order(const typename Comb::Part *part,
+                                                              uint64_t stride, uint32_t segs) {
+  using Part = typename Comb::Part;
+  constexpr uint32_t kBatch = 16;
+  Part p = part[0];
+  uint32_t s = 1;
+  for (; s + kBatch <= segs; s += kBatch) {
+    Part q[kBatch];
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i) q[i] = part[uint64_t(s + i) * stride];
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i) p = Comb::merge(p, q[i]);
+  }
+  for (; s < segs; ++s) p = Comb::merge(p, part[uint64_t(s) * stride]);
+  return p;
+}
+
 template <class Comb>
 __global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
   using Part = typename Comb::Part;
   const uint64_t row = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (row >= A.rows) return;
   const Part *part = static_cast<const Part *>(A.part) + row * A.segs;
-  Part p = part[0];
-  for (uint32_t s = 1; s < A.segs; ++s) p = Comb::merge(p, part[s]);
+  const Part p = merge_in_order<Comb>(part, 1, A.segs);
   int64_t base[1], tbase;
   decode_outer(A, uint32_t(row), base, tbase);
   store_final<Comb>(A.out, tbase, p, A.post, A.divisor);
@@ -402,10 +424,16 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   __shared__ Fast sh[kBlock / 64][64 * W];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t o = blockIdx.x / xblocks;
-  const uint64_t j = (uint64_t(blockIdx.x - o * xblocks) * 64 + lane) * W;
+  uint32_t bx = blockIdx.x, chunk = blockIdx.y;
+  if constexpr (PLAST_RED_XCD != 0) {
+    // renumber the (x, chunk) grid in dispatch order (x fastest)
+    const uint32_t lin = xcd_block(chunk * gridDim.x + bx, gridDim.x * gridDim.y);
+    chunk = lin / gridDim.x;
+    bx = lin - chunk * gridDim.x;
+  }
+  const uint32_t o = bx / xblocks;
+  const uint64_t j = (uint64_t(bx - o * xblocks) * 64 + lane) * W;
   const bool active = j < A.inner;  // no early return: the workgroup meets at a barrier
-  const uint32_t chunk = blockIdx.y;
   int64_t base[NIN], tbase;
   decode_outer(A, o, base, tbase);
 #pragma unroll
@@ -509,9 +537,7 @@ __global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<1> A) {
   const uint64_t oi = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
   const uint64_t nout = A.rows * A.inner;
   if (oi >= nout) return;
-  const Part *part = static_cast<const Part *>(A.part);
-  Part p = part[oi];
-  for (uint32_t s = 1; s < A.segs; ++s) p = Comb::merge(p, part[uint64_t(s) * nout + oi]);
+  const Part p = merge_in_order<Comb>(static_cast<const Part *>(A.part) + oi, nout, A.segs);
   const uint32_t o = uint32_t(oi / A.inner);
   const uint64_t j = oi - uint64_t(o) * A.inner;
   int64_t base[1], tbase;

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_flat_kernel(const float *__re
                                                                const float *__restrict__ dloss,
                                                                float *dx, MagicDiv dc4,
                                                                uint32_t units) {
-  const uint32_t q = blockIdx.x * kCeBlock + threadIdx.x;
+  const uint32_t q = (PLAST_CE_BWD_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x) * kCeBlock + threadIdx.x;
   if (q >= units) return;
   const uint32_t row = dc4.div(q);
   const uint32_t j4 = q - row * dc4.d;
