@@ -37,6 +37,18 @@ class T:
     def shape(self):
         return list(abi.shape_of(self.dev.t))
 
+    @property
+    def ndim(self):
+        return len(self.shape)
+
+    def numel(self):
+        return int(np.prod(self.shape))
+
+    def item(self):
+        """tensor.py:299-310: the one element as a Python float."""
+        assert self.numel() == 1
+        return float(self.numpy().reshape(-1)[0])
+
     # ---------------------------------------------------------------- construction helpers
     def _op(self, op, inputs, shape, p=None):
         rg = any(x.requires_grad for x in inputs)
@@ -80,6 +92,8 @@ class T:
     def _red(self, op, dim=None, keepdim=False):
         if dim is None:
             return self._op(op, [self], [1], KernelParams(DIM_ALL, 0, 0.0))
+        if dim < 0:
+            dim += self.ndim
         shape = list(self.shape)
         if keepdim:
             shape[dim] = 1
@@ -105,12 +119,21 @@ class T:
     reshape = view
 
     def transpose(self, d0, d1):
+        d0, d1 = d0 % self.ndim, d1 % self.ndim   # tensor.py:716-725
         shape = list(self.shape)
         shape[d0], shape[d1] = shape[d1], shape[d0]
         return self._view_op("transpose", shape, KernelParams(d0, d1, 0.0))
 
-    def squeeze(self):
-        return self._view_op("squeeze", [s for s in self.shape if s != 1] or [1])
+    def squeeze(self, dim=None):
+        """tensor.py:758-771: every size-1 axis, or axis `dim` when it has size 1."""
+        if dim is None:
+            return self._view_op("squeeze", [s for s in self.shape if s != 1] or [1])
+        dim = dim % self.ndim
+        if self.shape[dim] != 1:
+            return self
+        shape = list(self.shape)
+        shape.pop(dim)
+        return self._view_op("squeeze", shape)
 
     def unsqueeze(self, dim):
         shape = list(self.shape)
@@ -152,6 +175,58 @@ class _GradView:
 
 def tensor(a, requires_grad=False) -> T:
     return T(DeviceTensor.from_numpy(np.ascontiguousarray(a, np.float32), requires_grad), requires_grad)
+
+
+# ------------------------------------------------------------- compositions of plast/nn/functional.py
+def relu(x: T) -> T:
+    """functional.py:24-26."""
+    return x.leaky_relu(0.0)
+
+
+def tanh(x: T) -> T:
+    """functional.py:48-54: (e^x - e^-x) / (e^x + e^-x), op by op."""
+    ex = x.exp()
+    enx = (-x).exp()
+    return (ex - enx) / (ex + enx)
+
+
+def softmax(x: T, dim: int = -1) -> T:
+    """functional.py:77-86."""
+    shifted = x - x.max(dim=dim, keepdim=True)
+    e = shifted.exp()
+    return e / e.sum(dim=dim, keepdim=True)
+
+
+def log_softmax(x: T, dim: int = -1) -> T:
+    """functional.py:89-97."""
+    shifted = x - x.max(dim=dim, keepdim=True)
+    return shifted - shifted.exp().sum(dim=dim, keepdim=True).log()
+
+
+def _reduce(loss: T, reduction: str) -> T:
+    """functional.py:391-396."""
+    return loss.mean() if reduction == "mean" else loss.sum() if reduction == "sum" else loss
+
+
+def mse_loss(pred: T, target: T, reduction: str = "mean") -> T:
+    """functional.py:279-284."""
+    d = pred - target
+    return _reduce(d * d, reduction)
+
+
+def l1_loss(pred: T, target: T, reduction: str = "mean") -> T:
+    """functional.py:287-291."""
+    return _reduce(abs(pred - target), reduction)
+
+
+def cross_entropy(logits: T, labels: np.ndarray, reduction: str = "mean") -> T:
+    """functional.py:312-333 with class indices: a dense one-hot built on the host, then
+    -(onehot * log_softmax(x, 1)).sum(1), reduced."""
+    n, c = logits.shape
+    onehot = np.zeros((n, c), np.float32)
+    onehot[np.arange(n), labels] = 1.0
+    loss = -(tensor(onehot) * log_softmax(logits, dim=1)).sum(dim=1)
+    return _reduce(loss, reduction)
 
 
 def forward(t: T) -> None:

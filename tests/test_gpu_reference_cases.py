@@ -4,8 +4,9 @@ Each case keeps the reference test's inputs (np.random.RandomState(42) per test,
 fixture: tests/conftest.py:56-58), its op sequence and its numpy closed form, and its tolerance
 (rtol 1e-3 / atol 1e-4: conftest.py:5-6; exp at atol 1e-3). Sources:
 tests/test_ops.py:18-189, 205-287, 407-433 (elementwise, reductions, shape ops, leaky relu, ops with
-gradients) and tests/test_gradients.py:20-188 (autograd basics and per-op gradients). Matmul and
-conv cases are out of this path. The expressions run through reference_api, which builds the DAG
+gradients) and tests/test_gradients.py:20-188 (autograd basics and per-op gradients), tests/test_edge_cases.py:6-147
+(small shapes, broadcasts, op chains, view ops) and tests/test_nn.py:35-110 (activations and losses
+composed of these ops: plast/nn/functional.py). Matmul, conv and Linear cases are out of this path. The expressions run through reference_api, which builds the DAG
 of `<op>_hip_forward/backward` nodes."""
 from __future__ import annotations
 
@@ -265,3 +266,162 @@ def test_unary_grad(P, rng, op):
         close(x.grad.numpy(), want, atol=1e-4)
     else:
         close(x.grad.numpy(), want)
+
+
+# ------------------------------------------------------------------ test_edge_cases.py
+def test_single_element_tensor(P):
+    a = P.tensor(np.array([42.0], dtype=np.float32))
+    assert a.item() == 42.0 and a.shape == [1] and a.numel() == 1
+
+
+def test_scalar_arithmetic(P):
+    c = P.tensor(np.array([3.0], np.float32)) + P.tensor(np.array([2.0], np.float32))
+    P.forward(c)
+    close(c.numpy(), [5.0])
+
+
+def test_large_tensor_creation_and_high_dim(P, rng):
+    a = P.tensor(np.zeros((100, 100), np.float32))
+    assert a.shape == [100, 100] and a.numel() == 10000
+    b = P.tensor(rng.randn(2, 3, 4, 5).astype(np.float32))
+    assert b.ndim == 4 and b.shape == [2, 3, 4, 5]
+
+
+@pytest.mark.parametrize("sa, sb", [((3, 1), (1, 4)), ((4, 1), (1, 4))])
+def test_broadcast_add_outer(P, rng, sa, sb):
+    a, b = rng.randn(*sa).astype(np.float32), rng.randn(*sb).astype(np.float32)
+    c = P.tensor(a) + P.tensor(b)
+    P.forward(c)
+    close(c.numpy(), a + b)
+
+
+def test_multiple_ops_chain(P, rng):
+    """(a + b) * c -> sin -> sum, backward; the reference checks the grads exist, the closed forms
+    pin them: d/da = d/db = cos((a+b)c) c, d/dc = cos((a+b)c) (a+b)."""
+    a, b, c = (rng.randn(2, 3).astype(np.float32) for _ in range(3))
+    ta, tb, tc = (P.tensor(x, True) for x in (a, b, c))
+    loss = ((ta + tb) * tc).sin().sum()
+    P.forward(loss)
+    loss.backward()
+    s = (a + b).astype(np.float32)
+    g = np.cos(s * c)
+    close(ta.grad.numpy(), g * c)
+    close(tb.grad.numpy(), g * c)
+    close(tc.grad.numpy(), g * s)
+
+
+def test_grad_non_requires_grad_input(P, rng):
+    a = P.tensor(rng.randn(3).astype(np.float32), True)
+    b = P.tensor(rng.randn(3).astype(np.float32), False)
+    loss = (a + b).sum()
+    P.forward(loss)
+    loss.backward()
+    assert a.grad is not None and b.grad is None
+    close(a.grad.numpy(), np.ones(3))
+
+
+def test_tensor_arithmetic_chain(P, rng):
+    a, b, c = (rng.randn(2, 3).astype(np.float32) for _ in range(3))
+    one = np.ones((2, 3), np.float32)
+    ta, tb, tc, to = (P.tensor(x) for x in (a, b, c, one))
+    d = (ta + tb) * tc - ta / (tb + to)
+    P.forward(d)
+    close(d.numpy(), (a + b) * c - a / (b + 1.0))
+
+
+def test_unsqueeze_chain(P, rng):
+    a = rng.randn(3).astype(np.float32)
+    tb = P.tensor(a).unsqueeze(0).unsqueeze(2)
+    P.forward(tb)
+    assert tb.shape == [1, 3, 1]
+    close(tb.numpy(), a[np.newaxis, :, np.newaxis])
+
+
+def test_squeeze_all_and_dim(P, rng):
+    a = rng.randn(1, 3, 1, 4, 1).astype(np.float32)
+    tb = P.tensor(a).squeeze()
+    P.forward(tb)
+    close(tb.numpy(), a.reshape(3, 4))
+    a2 = rng.randn(1, 3, 1, 4).astype(np.float32)
+    tc = P.tensor(a2).squeeze(dim=0)
+    P.forward(tc)
+    assert tc.shape == [3, 1, 4]
+    close(tc.numpy(), a2.reshape(3, 1, 4))
+
+
+@pytest.mark.parametrize("dims", [(-2, -1), (1, 2)])
+def test_transpose_last_two(P, rng, dims):
+    a = rng.randn(2, 3, 4).astype(np.float32)
+    tb = P.tensor(a).transpose(*dims)
+    P.forward(tb)
+    close(tb.numpy(), np.transpose(a, (0, 2, 1)))
+
+
+def test_view_then_op(P, rng):
+    a = rng.randn(2, 6).astype(np.float32)
+    b = rng.randn(4).astype(np.float32)
+    tc = P.tensor(a).view(3, 4) + P.tensor(b)
+    P.forward(tc)
+    close(tc.numpy(), a.reshape(3, 4) + b)
+
+
+# ------------------------------------------------------------------ test_nn.py: activations, losses
+def test_relu_forward(P, rng):
+    x = rng.randn(2, 3).astype(np.float32)
+    out = P.relu(P.tensor(x))
+    P.forward(out)
+    close(out.numpy(), np.maximum(x, 0))
+
+
+def test_tanh_forward(P, rng):
+    x = rng.randn(2, 3).astype(np.float32)
+    out = P.tanh(P.tensor(x))
+    P.forward(out)
+    close(out.numpy(), np.tanh(x), atol=1e-3)
+
+
+def test_leaky_relu_module(P, rng):
+    x = rng.randn(2, 3).astype(np.float32)
+    out = P.tensor(x).leaky_relu(0.02)
+    P.forward(out)
+    close(out.numpy(), np.where(x > 0, x, 0.02 * x))
+
+
+def test_softmax(P, rng):
+    x = rng.randn(2, 4).astype(np.float32)
+    out = P.softmax(P.tensor(x), dim=1)
+    P.forward(out)
+    close(out.numpy(), np.exp(x) / np.sum(np.exp(x), axis=1, keepdims=True))
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_mse_loss(P, rng, reduction):
+    pred, target = rng.randn(4, 1).astype(np.float32), rng.randn(4, 1).astype(np.float32)
+    loss = P.mse_loss(P.tensor(pred), P.tensor(target), reduction)
+    P.forward(loss)
+    d = pred - target
+    close(loss.numpy(), np.array([np.mean(d ** 2) if reduction == "mean" else np.sum(d ** 2)]))
+
+
+def test_l1_loss(P, rng):
+    pred, target = rng.randn(4, 1).astype(np.float32), rng.randn(4, 1).astype(np.float32)
+    loss = P.l1_loss(P.tensor(pred), P.tensor(target))
+    P.forward(loss)
+    close(loss.numpy(), np.array([np.mean(np.abs(pred - target))]))
+
+
+def test_cross_entropy_loss(P, rng):
+    """The composed chain (functional.py:312-333) at the reference's atol 1e-2, and the fused
+    softmax_cross_entropy op's mean row loss on the same logits."""
+    from plast_amd import ops, runtime as rt
+    logits = rng.randn(3, 5).astype(np.float32)
+    labels = np.array([0, 2, 4], dtype=np.int32)
+    loss = P.cross_entropy(P.tensor(logits), labels)
+    P.forward(loss)
+    e = np.exp(logits - logits.max(1, keepdims=True))
+    sm = e / e.sum(1, keepdims=True)
+    want = -np.mean(np.log(sm[np.arange(3), labels] + 1e-8))
+    close(loss.numpy(), np.array([want]), atol=1e-2)
+    rows, _ = ops.softmax_cross_entropy(rt.DeviceTensor.from_numpy(logits),
+                                        rt.DeviceTensor.from_numpy(labels))
+    close(np.array([rows.numpy().mean()]), loss.numpy(), rtol=1e-5, atol=1e-6)
