@@ -5,6 +5,7 @@
 #include <type_traits>
 #include <utility>
 
+#include "chain_jit.hpp"
 #include "ew.hpp"
 
 namespace plast {
@@ -601,6 +602,13 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.units = n / 4;
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
+    if constexpr (Body::kTape) {
+      // a flat chain over streamed inputs and broadcast scalars: its compiled form, one float4 per
+      // lane (false when the chain compiler does not take it; the interpreter below then runs)
+      if (in_ax == 0 && (A.reused & ~A.bcast_inner) == 0 &&
+          chain_jit_launch(body.t, A.in, A.bcast_inner, A.out, A.units, body.simd_end))
+        return true;
+    }
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
     const bool done = (A.reused & ~A.bcast_inner) != 0 ? launch_vec<Body, true>(A, body, in_ax)
                                                        : launch_vec<Body, false>(A, body, in_ax);

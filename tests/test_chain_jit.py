@@ -1,0 +1,85 @@
+"""CPU checks of the chain compiler: the source it writes for each case of chain_cases.TAPES
+compiles with hiprtc for gfx950 under the library's own flags (no device needed), and spells out
+each tape instruction as the interpreter's statement for it (TapeBody::eval_units in ew.hpp)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import pytest
+
+from chain_cases import TAPES
+from plast_amd import abi
+from plast_amd.ops import make_tape
+
+try:
+    RTC = C.CDLL("libhiprtc.so.7")
+except OSError:
+    RTC = None
+
+
+_L = []
+
+
+def _lib():
+    """The library without device initialisation (the source writer needs no device)."""
+    if not _L:
+        from plast_amd.runtime import Library
+        _L.append(Library())
+    return _L[0]
+
+
+def source(ins, nin, bcast) -> str:
+    tape = make_tape(ins, nin)
+    L = _lib()
+    n = L.plast_hip_chain_jit_source(C.addressof(tape), bcast, None, 0)
+    assert n > 0
+    buf = C.create_string_buffer(int(n) + 1)
+    assert L.plast_hip_chain_jit_source(C.addressof(tape), bcast, buf, n + 1) == n
+    return buf.value.decode()
+
+
+def test_malformed_tape_gives_no_source():
+    tape = abi.FusedTape()
+    assert _lib().plast_hip_chain_jit_source(C.addressof(tape), 0, None, 0) == 0
+
+
+def test_config2_statements():
+    name, nin, bcast, ins = TAPES[0]
+    s = source(ins, nin, bcast)
+    body = [l.strip() for l in s.splitlines() if l.strip().startswith("a = ")]
+    assert body == ["a = a * x1[c];", "a = a + x2[c];", "a = a > 0.0f ? a : a * A.imm[3];",
+                    "a = simd ? 0.0f - a : -a;", "a = expf(a);"]
+    assert "float a = x0[c];" in s
+    assert s.count("__builtin_nontemporal_load") == 3
+
+
+def test_operand_orders_and_broadcast_scalars():
+    s = source(TAPES[1][3], 2, 0)
+    body = [l.strip() for l in s.splitlines() if l.strip().startswith("a = ")]
+    assert body == ["a = x0[c] - a;", "a = a / x1[c];", "a = a - A.imm[3];", "a = A.imm[4] / a;",
+                    "a = a + a;"]
+    s = source(TAPES[4][3], 4, 0b1010)
+    assert "const f4 x1 = f4(A.in[1][0]);" in s and "const f4 x3 = f4(A.in[3][0]);" in s
+    assert s.count("__builtin_nontemporal_load") == 2
+
+
+@pytest.mark.skipif(RTC is None, reason="libhiprtc not present")
+@pytest.mark.parametrize("case", TAPES, ids=[t[0] for t in TAPES])
+def test_generated_source_compiles_for_gfx950(case):
+    name, nin, bcast, ins = case
+    src = source(ins, nin, bcast).encode()
+    prog = C.c_void_p()
+    assert RTC.hiprtcCreateProgram(C.byref(prog), src, b"plast_chain.hip", 0, None, None) == 0
+    opts = [b"--offload-arch=gfx950", b"-O3", b"-std=c++17", b"-ffp-contract=off",
+            b"-Xclang", b"-target-feature", b"-Xclang", b"-packed-fp32-ops"]
+    arr = (C.c_char_p * len(opts))(*opts)
+    rc = RTC.hiprtcCompileProgram(prog, len(opts), arr)
+    size = C.c_size_t(0)
+    RTC.hiprtcGetProgramLogSize(prog, C.byref(size))
+    log = C.create_string_buffer(size.value + 1)
+    RTC.hiprtcGetProgramLog(prog, log)
+    code = C.c_size_t(0)
+    RTC.hiprtcGetCodeSize(prog, C.byref(code))
+    RTC.hiprtcDestroyProgram(C.byref(prog))
+    assert rc == 0, log.value.decode(errors="replace")
+    assert code.value > 1000
