@@ -3,12 +3,15 @@
 // The tape interpreter (TapeBody) pays one instruction dispatch per tape step and per evaluation, so
 // it evaluates two float4 units per lane to amortise that; the shape that streams fastest on MI355X
 // is one float4 per lane with XCD-contiguous workgroups, where the dispatch would be paid per unit.
-// For flat spaces of at least kMinUnits float4 units this file writes the tape out as HIP source —
-// the same per-element operations in the same order, through the same ocml functions, compiled
-// with contraction off — compiles it once per distinct tape with hiprtc for the device's
-// architecture, and launches it with the one-unit shape. Immediates are kernel arguments, so tapes
-// that differ only in constants share one kernel. Compiled modules stay loaded until the process
-// ends. The fused op's semantics are unchanged: every result bit equals the interpreter's.
+// For spaces of at least kMinUnits float4 units this file writes the tape out as HIP source — the
+// interpreter's statement for each instruction, component by component, through the same ocml
+// functions, compiled with the library's flags (contraction off, no packed fp32) — compiles it once
+// per distinct tape and launch form with hiprtc for the device's architecture, and launches it:
+//  - flat form: inputs unit-stride or broadcast scalars, one float4 per lane;
+//  - tile form: the transposed-operand tile of ew_tile_fixed_kernel (64x64 tiles, operand roles
+//    fixed per kernel) with the tape inlined per output row.
+// Immediates are kernel arguments, so tapes that differ only in constants share a kernel. Compiled
+// modules stay loaded until the process ends. Every result bit equals the interpreter's.
 #include <hip/hiprtc.h>
 
 #include <cstdio>
@@ -22,20 +25,46 @@
 #include "chain_jit.hpp"
 #include "common.hpp"
 
+// The kernels' parameter blocks. Each is declared once here and pasted as text into the generated
+// source, so host and device agree on the layout.
+#define PLAST_JIT_FLAT_ARGS                                                                        \
+  struct JitArgs {                                                                                 \
+    const float *in[4];                                                                            \
+    float *out;                                                                                    \
+    unsigned long long units;                                                                      \
+    unsigned long long simd_end;                                                                   \
+    float imm[16];                                                                                 \
+  };
+#define PLAST_JIT_TILE_ARGS                                                                        \
+  struct JitTileArgs {                                                                             \
+    const float *in[4];                                                                            \
+    float *out;                                                                                    \
+    long long bst[5][8];                                                                           \
+    unsigned bdv[8][3];                                                                            \
+    long long qst[5];                                                                              \
+    long long pst[5];                                                                              \
+    unsigned nbatch;                                                                               \
+    unsigned tq;                                                                                   \
+    unsigned tp;                                                                                   \
+    unsigned dtq[3];                                                                               \
+    unsigned dtp[3];                                                                               \
+    unsigned long long simd_end;                                                                   \
+    float imm[16];                                                                                 \
+  };
+#define PLAST_JIT_STR2(...) #__VA_ARGS__
+#define PLAST_JIT_STR(...) PLAST_JIT_STR2(__VA_ARGS__)
+
 namespace plast {
 namespace {
 
-constexpr uint64_t kMinUnits = uint64_t(1) << 18;  // 2^20 elements: below that, compiling costs more
-constexpr int kJitBlock = 256;
+PLAST_JIT_FLAT_ARGS
+PLAST_JIT_TILE_ARGS
+static_assert(PLAST_TAPE_MAX_INPUTS == 4 && PLAST_TAPE_MAX_INS == 16 && PLAST_MAX_NDIM == 8,
+              "the parameter blocks above are written for these limits");
 
-// The generated kernel's parameter block (its source declares the same struct).
-struct JitArgs {
-  const float *in[PLAST_TAPE_MAX_INPUTS];
-  float *out;
-  uint64_t units;
-  uint64_t simd_end;
-  float imm[PLAST_TAPE_MAX_INS];
-};
+constexpr uint64_t kMinUnits = uint64_t(1) << 18;  // 2^20 elements: below that, compiling costs more
+constexpr int kJitBlock = 256;                     // lanes per workgroup, both forms
+constexpr int kJitTile = 64, kJitTilePad = 1;      // the interpreter's tile (kTile, kTilePad)
 
 struct Entry {
   hipModule_t mod = nullptr;
@@ -57,12 +86,13 @@ int mode_locked() {
   return g_mode;
 }
 
-// What the generated code depends on: inputs, broadcast pattern and every instruction but its
-// immediate.
-std::string key_of(const PlastFusedTape &t, uint32_t bcast, int device) {
+// What the generated code depends on: the form and its layout pattern, the inputs and every
+// instruction but its immediate.
+std::string key_of(char form, uint32_t pattern, const PlastFusedTape &t, int device) {
   std::string k;
+  k.push_back(form);
+  k.append(reinterpret_cast<const char *>(&pattern), sizeof pattern);
   k.push_back(char(t.num_inputs));
-  k.push_back(char(bcast));
   k.push_back(char(device));
   for (uint32_t i = 0; i < t.num_ins; ++i) {
     k.push_back(char(t.ins[i].op));
@@ -80,20 +110,52 @@ std::string operand(const PlastTapeIns &ins, int i) {
   return "a";  // TAPE_SRC_ACC, and TAPE_SRC_NONE as the interpreter reads it
 }
 
-// Per instruction the interpreter's case (TapeBody::eval_units in ew.hpp), component by component.
-std::string source_of(const PlastFusedTape &t, uint32_t bcast) {
-  const std::string NI = std::to_string(PLAST_TAPE_MAX_INPUTS), NS = std::to_string(PLAST_TAPE_MAX_INS);
+// The tape over component c of the float4 operands x0..x3, into `dst`[c]: per instruction the
+// interpreter's case (TapeBody::eval_units in ew.hpp). `simd` names the NEG rule's side.
+std::string tape_loop(const PlastFusedTape &t, const std::string &dst, const std::string &ind) {
   std::string s;
-  s += "typedef float f4 __attribute__((ext_vector_type(4)));\n";
-  s += "struct JitArgs { const float *in[" + NI + "]; float *out; unsigned long long units;\n";
-  s += "  unsigned long long simd_end; float imm[" + NS + "]; };\n";
+  s += ind + "for (int c = 0; c < 4; ++c) {\n";
+  const std::string in2 = ind + "  ";
+  s += in2 + "float a = x" + std::to_string(t.ins[0].idx) + "[c];\n";
+  for (uint32_t i = 1; i < t.num_ins; ++i) {
+    const PlastTapeIns &ins = t.ins[i];
+    const std::string o = operand(ins, int(i)), I = std::to_string(i);
+    switch (ins.op) {
+    case TAPE_ADD: s += in2 + "a = a + " + o + ";\n"; break;
+    case TAPE_MUL: s += in2 + "a = a * " + o + ";\n"; break;
+    case TAPE_SUB: s += in2 + (ins.acc_rhs ? "a = " + o + " - a;\n" : "a = a - " + o + ";\n"); break;
+    case TAPE_DIV: s += in2 + (ins.acc_rhs ? "a = " + o + " / a;\n" : "a = a / " + o + ";\n"); break;
+    case TAPE_LEAKY_RELU: s += in2 + "a = a > 0.0f ? a : a * A.imm[" + I + "];\n"; break;
+    case TAPE_EXP: s += in2 + "a = expf(a);\n"; break;
+    case TAPE_LOG: s += in2 + "a = logf(a);\n"; break;
+    case TAPE_NEG: s += in2 + "a = simd ? 0.0f - a : -a;\n"; break;
+    case TAPE_ABS: s += in2 + "a = fabsf(a);\n"; break;
+    case TAPE_SIN: s += in2 + "a = sinf(a);\n"; break;
+    case TAPE_COS: s += in2 + "a = cosf(a);\n"; break;
+    case TAPE_TAN: s += in2 + "a = tanf(a);\n"; break;
+    default: break;  // a later TAPE_LOAD is a no-op in the interpreter too
+    }
+  }
+  s += in2 + dst + "[c] = a;\n";
+  s += ind + "}\n";
+  return s;
+}
+
+const std::string kPrelude = "typedef float f4 __attribute__((ext_vector_type(4)));\n";
+
+// XCD-contiguous numbering of the first 8 * (grid / 8) workgroups (xcd_block in common.hpp).
+const std::string kXcdBlock =
+    "  const unsigned per = gridDim.x / 8;\n"
+    "  unsigned bid = blockIdx.x;\n"
+    "  if (bid < per * 8) bid = (bid % 8) * per + bid / 8;\n";
+
+// Flat form: bit k of bcast marks input k as one broadcast scalar.
+std::string flat_source(const PlastFusedTape &t, uint32_t bcast) {
+  std::string s = kPrelude + PLAST_JIT_STR(PLAST_JIT_FLAT_ARGS) + "\n";
   s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(kJitBlock) +
        ") void plast_chain(JitArgs A) {\n";
-  // XCD-contiguous numbering of the first 8 * (grid / 8) workgroups (xcd_block in common.hpp)
-  s += "  const unsigned per = gridDim.x / 8;\n";
-  s += "  unsigned b = blockIdx.x;\n";
-  s += "  if (b < per * 8) b = (b % 8) * per + b / 8;\n";
-  s += "  const unsigned long long q = (unsigned long long)b * " + std::to_string(kJitBlock) +
+  s += kXcdBlock;
+  s += "  const unsigned long long q = (unsigned long long)bid * " + std::to_string(kJitBlock) +
        " + threadIdx.x;\n";
   s += "  if (q >= A.units) return;\n";
   s += "  const bool simd = q * 4 < A.simd_end;\n";
@@ -107,30 +169,113 @@ std::string source_of(const PlastFusedTape &t, uint32_t bcast) {
     s += "  (void)x" + K + ";\n";
   }
   s += "  f4 r;\n";
-  s += "  for (int c = 0; c < 4; ++c) {\n";
-  s += "    float a = x" + std::to_string(t.ins[0].idx) + "[c];\n";
-  for (uint32_t i = 1; i < t.num_ins; ++i) {
-    const PlastTapeIns &ins = t.ins[i];
-    const std::string o = operand(ins, int(i)), I = std::to_string(i);
-    switch (ins.op) {
-    case TAPE_ADD: s += "    a = a + " + o + ";\n"; break;
-    case TAPE_MUL: s += "    a = a * " + o + ";\n"; break;
-    case TAPE_SUB: s += ins.acc_rhs ? "    a = " + o + " - a;\n" : "    a = a - " + o + ";\n"; break;
-    case TAPE_DIV: s += ins.acc_rhs ? "    a = " + o + " / a;\n" : "    a = a / " + o + ";\n"; break;
-    case TAPE_LEAKY_RELU: s += "    a = a > 0.0f ? a : a * A.imm[" + I + "];\n"; break;
-    case TAPE_EXP: s += "    a = expf(a);\n"; break;
-    case TAPE_LOG: s += "    a = logf(a);\n"; break;
-    case TAPE_NEG: s += "    a = simd ? 0.0f - a : -a;\n"; break;
-    case TAPE_ABS: s += "    a = fabsf(a);\n"; break;
-    case TAPE_SIN: s += "    a = sinf(a);\n"; break;
-    case TAPE_COS: s += "    a = cosf(a);\n"; break;
-    case TAPE_TAN: s += "    a = tanf(a);\n"; break;
-    default: break;  // a later TAPE_LOAD is a no-op in the interpreter too
+  s += tape_loop(t, "r", "  ");
+  s += "  ((f4 *)A.out)[q] = r;\n";
+  s += "}\n";
+  return s;
+}
+
+// Tile form: the structure of ew_tile_fixed_kernel (ew_impl.hpp) with compile-time roles. Every
+// global read of the tile is issued before the barrier; the transposed operands go through LDS.
+std::string tile_source(const PlastFusedTape &t, uint32_t roles) {
+  const int nin = int(t.num_inputs), OUT = PLAST_TAPE_MAX_INPUTS;
+  const std::string T = std::to_string(kJitTile), TP = std::to_string(kJitTile + kJitTilePad),
+                    O = std::to_string(OUT);
+  auto role = [&](int k) { return (roles >> (2 * k)) & 3u; };
+  auto tile_at = [&](int slot) { return std::to_string(slot * kJitTile * (kJitTile + kJitTilePad)); };
+  std::string s = kPrelude + PLAST_JIT_STR(PLAST_JIT_TILE_ARGS) + "\n";
+  s += "static __device__ __forceinline__ unsigned mdiv(unsigned n, const unsigned *m) {\n"
+       "  const unsigned long long hi = __umulhi(n, m[0]);\n"
+       "  return (unsigned)((hi + n) >> m[1]);\n"
+       "}\n";
+  s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(kJitBlock) +
+       ") void plast_chain_tile(JitTileArgs A) {\n";
+  s += "  extern __shared__ float lds[];\n";
+  s += kXcdBlock;
+  s += "  const unsigned bq = mdiv(bid, A.dtp);\n"
+       "  const unsigned tpi = bid - bq * A.tp;\n"
+       "  const unsigned bi = mdiv(bq, A.dtq);\n"
+       "  const unsigned tqi = bq - bi * A.tq;\n";
+  s += "  long long base[" + std::to_string(OUT + 1) + "] = {};\n";
+  s += "  unsigned rem = bi;\n";
+  s += "  for (int d = (int)A.nbatch - 1; d >= 0; --d) {\n"
+       "    const unsigned nxt = mdiv(rem, A.bdv[d]);\n"
+       "    const long long c = (long long)(rem - nxt * A.bdv[d][2]);\n"
+       "    rem = nxt;\n";
+  for (int k = 0; k < nin; ++k)
+    s += "    base[" + std::to_string(k) + "] += c * A.bst[" + std::to_string(k) + "][d];\n";
+  s += "    base[" + O + "] += c * A.bst[" + O + "][d];\n";
+  s += "  }\n";
+  s += "  const long long q0 = (long long)tqi * " + T + ", p0 = (long long)tpi * " + T + ";\n";
+  s += "  const int t = threadIdx.x;\n";
+  s += "  const unsigned l4 = (t & 15) * 4, r16 = t >> 4;\n";
+  s += "  const bool simd = 0 < A.simd_end;\n";
+  s += "  (void)simd;\n";
+  int slot = 0;
+  std::vector<int> slot_of(nin, -1);
+  for (int k = 0; k < nin; ++k) {
+    const std::string K = std::to_string(k);
+    const std::string in = "A.in[" + K + "] + base[" + K + "]";
+    switch (role(k)) {
+    case 0:  // staged: float4 along q of tile rows p0 + r16 + 16r, nontemporal
+      slot_of[k] = slot++;
+      s += "  f4 v" + K + "[4];\n";
+      s += "  { const float *src = " + in + " + (q0 + l4) * A.qst[" + K + "] + (p0 + r16) * A.pst[" +
+           K + "];\n";
+      s += "    const long long step = 16 * A.pst[" + K + "];\n";
+      s += "    for (int r = 0; r < 4; ++r) v" + K +
+           "[r] = __builtin_nontemporal_load((const f4 *)(src + r * step)); }\n";
+      break;
+    case 1:  // the scalar of each output row q0 + r16 + 16r
+      s += "  float v" + K + "[4];\n";
+      s += "  { const float *src = " + in + " + (q0 + r16) * A.qst[" + K + "];\n";
+      s += "    const long long step = 16 * A.qst[" + K + "];\n";
+      s += "    for (int r = 0; r < 4; ++r) v" + K + "[r] = src[r * step]; }\n";
+      break;
+    case 2:  // one float4 along p
+      s += "  const f4 v" + K + " = *(const f4 *)(" + in + " + (p0 + l4) * A.pst[" + K + "]);\n";
+      break;
+    default:  // float4 along p of each output row
+      s += "  f4 v" + K + "[4];\n";
+      s += "  { const float *src = " + in + " + (q0 + r16) * A.qst[" + K + "] + (p0 + l4);\n";
+      s += "    const long long step = 16 * A.qst[" + K + "];\n";
+      s += "    for (int r = 0; r < 4; ++r) v" + K + "[r] = *(const f4 *)(src + r * step); }\n";
+      break;
     }
   }
-  s += "    r[c] = a;\n";
+  for (int k = 0; k < nin; ++k) {
+    if (slot_of[k] < 0) continue;
+    const std::string K = std::to_string(k);
+    s += "  { float *tile = lds + " + tile_at(slot_of[k]) + ";\n";
+    s += "    for (int r = 0; r < 4; ++r)\n";
+    s += "      for (int c = 0; c < 4; ++c) tile[(r16 + 16 * r) * " + TP + " + l4 + c] = v" + K +
+         "[r][c]; }\n";
+  }
+  s += "  __syncthreads();\n";
+  s += "  float *dst = A.out + base[" + O + "] + (q0 + r16) * A.qst[" + O + "] + (p0 + l4);\n";
+  s += "  const long long dstep = 16 * A.qst[" + O + "];\n";
+  s += "#pragma unroll\n";
+  s += "  for (int r = 0; r < 4; ++r) {\n";
+  s += "    const unsigned row = r16 + 16 * r;\n";
+  s += "    (void)row;\n";
+  for (int k = 0; k < nin; ++k) {
+    const std::string K = std::to_string(k);
+    switch (role(k)) {
+    case 0:
+      s += "    f4 x" + K + ";\n";
+      s += "    { const float *tile = lds + " + tile_at(slot_of[k]) + ";\n";
+      s += "      for (int c = 0; c < 4; ++c) x" + K + "[c] = tile[(l4 + c) * " + TP + " + row]; }\n";
+      break;
+    case 1: s += "    const f4 x" + K + " = f4(v" + K + "[r]);\n"; break;
+    case 2: s += "    const f4 x" + K + " = v" + K + ";\n"; break;
+    default: s += "    const f4 x" + K + " = v" + K + "[r];\n"; break;
+    }
+    s += "    (void)x" + K + ";\n";
+  }
+  s += "    f4 res;\n";
+  s += tape_loop(t, "res", "    ");
+  s += "    *(f4 *)(dst + r * dstep) = res;\n";
   s += "  }\n";
-  s += "  ((f4 *)A.out)[q] = r;\n";
   s += "}\n";
   return s;
 }
@@ -142,7 +287,7 @@ void log_once(const char *what, const std::string &detail) {
                        "interpreter%s%s\n", what, detail.empty() ? "" : ": ", detail.c_str());
 }
 
-bool compile(const std::string &src, int device, Entry &e) {
+bool compile(const std::string &src, const char *name, int device, Entry &e) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
     log_once("hipGetDeviceProperties", "");
@@ -174,12 +319,55 @@ bool compile(const std::string &src, int device, Entry &e) {
   hiprtcGetCode(p, code.data());
   hiprtcDestroyProgram(&p);
   if (hipModuleLoadData(&e.mod, code.data()) != hipSuccess ||
-      hipModuleGetFunction(&e.fn, e.mod, "plast_chain") != hipSuccess) {
+      hipModuleGetFunction(&e.fn, e.mod, name) != hipSuccess) {
     (void)hipGetLastError();
     log_once("hipModuleLoadData", "");
     return false;
   }
   return true;
+}
+
+// The cached kernel for (form, pattern, tape), compiling it on first use; null when unavailable.
+hipFunction_t kernel_for(char form, uint32_t pattern, const PlastFusedTape &t) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return nullptr;  // the library's device is current
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (!mode_locked()) return nullptr;
+  const std::string key = key_of(form, pattern, t, device);
+  auto it = g_cache.find(key);
+  if (it == g_cache.end()) {
+    Entry e;
+    e.ok = form == 'F' ? compile(flat_source(t, pattern), "plast_chain", device, e)
+                       : compile(tile_source(t, pattern), "plast_chain_tile", device, e);
+    it = g_cache.emplace(key, e).first;
+  }
+  return it->second.ok ? it->second.fn : nullptr;
+}
+
+bool launch(hipFunction_t fn, void *args, unsigned blocks, size_t lds_bytes) {
+  void *params[] = {args};
+  if (hipModuleLaunchKernel(fn, blocks, 1, 1, kJitBlock, 1, 1, unsigned(lds_bytes), stream(), params,
+                            nullptr) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  ++g_launches;
+  return true;
+}
+
+bool well_formed(const PlastFusedTape *t) {
+  return t && t->num_ins > 0 && t->num_ins <= PLAST_TAPE_MAX_INS && t->num_inputs > 0 &&
+         t->num_inputs <= PLAST_TAPE_MAX_INPUTS;
+}
+
+u64 copy_out(const std::string &src, char *buf, u64 cap) {
+  if (buf && cap) {
+    const size_t n = src.size() < cap - 1 ? src.size() : size_t(cap - 1);
+    std::memcpy(buf, src.data(), n);
+    buf[n] = '\0';
+  }
+  return src.size();
 }
 
 }  // namespace
@@ -189,37 +377,37 @@ bool chain_jit_launch(const PlastFusedTape &t, const float *const *in, uint32_t 
   if (units < kMinUnits) return false;
   const uint64_t blocks = (units + kJitBlock - 1) / kJitBlock;
   if (blocks > max_blocks(kJitBlock)) return false;
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return false;  // the library's device is current
-  hipFunction_t fn = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    if (!mode_locked()) return false;
-    const std::string key = key_of(t, bcast, device);
-    auto it = g_cache.find(key);
-    if (it == g_cache.end()) {
-      Entry e;
-      e.ok = compile(source_of(t, bcast), device, e);
-      it = g_cache.emplace(key, e).first;
-    }
-    if (!it->second.ok) return false;
-    fn = it->second.fn;
-  }
+  const hipFunction_t fn = kernel_for('F', bcast, t);
+  if (!fn) return false;
   JitArgs a = {};
   for (uint32_t k = 0; k < t.num_inputs; ++k) a.in[k] = in[k];
   a.out = out;
   a.units = units;
   a.simd_end = simd_end;
   for (uint32_t i = 0; i < t.num_ins; ++i) a.imm[i] = t.ins[i].imm;
-  void *params[] = {&a};
-  if (hipModuleLaunchKernel(fn, unsigned(blocks), 1, 1, kJitBlock, 1, 1, 0, stream(), params,
-                            nullptr) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  std::lock_guard<std::mutex> lock(g_mu);
-  ++g_launches;
-  return true;
+  return launch(fn, &a, unsigned(blocks), 0);
+}
+
+bool chain_jit_tile_launch(const PlastFusedTape &t, const ChainTileGeometry &g, uint32_t roles,
+                           uint64_t elements, uint64_t simd_end, unsigned blocks, size_t lds_bytes) {
+  if (elements / 4 < kMinUnits) return false;
+  const hipFunction_t fn = kernel_for('T', roles, t);
+  if (!fn) return false;
+  JitTileArgs a = {};
+  for (int k = 0; k < PLAST_TAPE_MAX_INPUTS; ++k) a.in[k] = g.in[k];
+  a.out = g.out;
+  std::memcpy(a.bst, g.bst, sizeof a.bst);
+  std::memcpy(a.bdv, g.bdv, sizeof a.bdv);
+  std::memcpy(a.qst, g.qst, sizeof a.qst);
+  std::memcpy(a.pst, g.pst, sizeof a.pst);
+  a.nbatch = g.nbatch;
+  a.tq = g.tq;
+  a.tp = g.tp;
+  std::memcpy(a.dtq, g.dtq, sizeof a.dtq);
+  std::memcpy(a.dtp, g.dtp, sizeof a.dtp);
+  a.simd_end = simd_end;
+  for (uint32_t i = 0; i < t.num_ins; ++i) a.imm[i] = t.ins[i].imm;
+  return launch(fn, &a, blocks, lds_bytes);
 }
 
 }  // namespace plast
@@ -241,16 +429,11 @@ u64 plast_hip_chain_jit_launches(void) {
 }
 
 u64 plast_hip_chain_jit_source(const PlastFusedTape *tape, u32 bcast, char *buf, u64 cap) {
-  if (!tape || tape->num_ins == 0 || tape->num_ins > PLAST_TAPE_MAX_INS ||
-      tape->num_inputs == 0 || tape->num_inputs > PLAST_TAPE_MAX_INPUTS)
-    return 0;
-  const std::string src = source_of(*tape, bcast);
-  if (buf && cap) {
-    const size_t n = src.size() < cap - 1 ? src.size() : size_t(cap - 1);
-    std::memcpy(buf, src.data(), n);
-    buf[n] = '\0';
-  }
-  return src.size();
+  return well_formed(tape) ? copy_out(flat_source(*tape, bcast), buf, cap) : 0;
+}
+
+u64 plast_hip_chain_jit_tile_source(const PlastFusedTape *tape, u32 roles, char *buf, u64 cap) {
+  return well_formed(tape) ? copy_out(tile_source(*tape, roles), buf, cap) : 0;
 }
 
 }  // extern "C"

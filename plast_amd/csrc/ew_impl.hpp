@@ -538,6 +538,34 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
   A.dtq = MagicDiv::make(A.tq);
   A.dtp = MagicDiv::make(A.tp);
   const bool full = A.eq % kTile == 0 && A.ep % kTile == 0;
+  if constexpr (Body::kTape) {
+    // whole tiles: the tape's compiled tile form, when the chain compiler takes it
+    if (full) {
+      ChainTileGeometry g;
+      memset(&g, 0, sizeof g);
+      for (int k = 0; k <= NIN; ++k) {
+        const int gk = k < NIN ? k : PLAST_TAPE_MAX_INPUTS;
+        if (k < NIN) g.in[k] = A.in[k];
+        for (int d = 0; d < nb; ++d) g.bst[gk][d] = A.bst[k][d];
+        g.qst[gk] = A.qst[k];
+        g.pst[gk] = A.pst[k];
+      }
+      g.out = A.out;
+      for (int d = 0; d < nb; ++d) {
+        g.bdv[d][0] = A.bdv[d].mul;
+        g.bdv[d][1] = A.bdv[d].shift;
+        g.bdv[d][2] = A.bdv[d].d;
+      }
+      g.nbatch = uint32_t(nb);
+      g.tq = A.tq;
+      g.tp = A.tp;
+      g.dtq[0] = A.dtq.mul, g.dtq[1] = A.dtq.shift, g.dtq[2] = A.dtq.d;
+      g.dtp[0] = A.dtp.mul, g.dtp[1] = A.dtp.shift, g.dtp[2] = A.dtp.d;
+      if (chain_jit_tile_launch(body.t, g, roles, s.numel(), body.simd_end, unsigned(blocks),
+                                lds_bytes))
+        return true;
+    }
+  }
   if (full && launch_tile_fixed(A, body, roles, unsigned(blocks), lds_bytes)) return true;
   if (direct) ew_tile_kernel<Body, true><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
   else ew_tile_kernel<Body, false><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);

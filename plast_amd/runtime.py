@@ -50,6 +50,7 @@ class Library:
             "plast_hip_set_chain_jit": ([C.c_int], C.c_int),
             "plast_hip_chain_jit_launches": ([], C.c_uint64),
             "plast_hip_chain_jit_source": ([C.c_void_p, C.c_uint32, C.c_char_p, C.c_uint64], C.c_uint64),
+            "plast_hip_chain_jit_tile_source": ([C.c_void_p, C.c_uint32, C.c_char_p, C.c_uint64], C.c_uint64),
             "plast_hip_synchronize": ([], C.c_int),
             "plast_hip_stream": ([], C.c_void_p),
             "plast_hip_error_count": ([], C.c_int),

@@ -28,14 +28,27 @@ def _lib():
     return _L[0]
 
 
-def source(ins, nin, bcast) -> str:
+def source(ins, nin, pattern, tile=False) -> str:
+    """The flat form's source (pattern: broadcast mask) or the tile form's (pattern: roles)."""
     tape = make_tape(ins, nin)
     L = _lib()
-    n = L.plast_hip_chain_jit_source(C.addressof(tape), bcast, None, 0)
+    f = L.plast_hip_chain_jit_tile_source if tile else L.plast_hip_chain_jit_source
+    n = f(C.addressof(tape), pattern, None, 0)
     assert n > 0
     buf = C.create_string_buffer(int(n) + 1)
-    assert L.plast_hip_chain_jit_source(C.addressof(tape), bcast, buf, n + 1) == n
+    assert f(C.addressof(tape), pattern, buf, n + 1) == n
     return buf.value.decode()
+
+
+def roles(*r):
+    return sum(v << (2 * k) for k, v in enumerate(r))
+
+
+# (tape case, roles): config 3's pattern and the others the fixed-role interpreter instantiates,
+# plus one that only the compiled form covers
+TILE_CASES = [(TAPES[0], roles(0, 1, 2)), (TAPES[0], roles(0, 3, 3)), (TAPES[0], roles(0, 0, 0)),
+              (TAPES[1], roles(0, 0)), (TAPES[1], roles(3, 0)), (TAPES[2], roles(0)),
+              (TAPES[3], roles(2, 0)), (TAPES[4], roles(0, 1, 3, 2))]
 
 
 def test_malformed_tape_gives_no_source():
@@ -63,11 +76,17 @@ def test_operand_orders_and_broadcast_scalars():
     assert s.count("__builtin_nontemporal_load") == 2
 
 
-@pytest.mark.skipif(RTC is None, reason="libhiprtc not present")
-@pytest.mark.parametrize("case", TAPES, ids=[t[0] for t in TAPES])
-def test_generated_source_compiles_for_gfx950(case):
-    name, nin, bcast, ins = case
-    src = source(ins, nin, bcast).encode()
+def test_tile_source_follows_roles():
+    (name, nin, _, ins), r = TILE_CASES[0]
+    s = source(ins, nin, r, tile=True)
+    assert s.count("__builtin_nontemporal_load") == 1          # operand 0 staged
+    assert "v1[r] = src[r * step]" in s                         # operand 1: scalar per row
+    assert "const f4 v2 = *(const f4 *)" in s                   # operand 2: one float4 along p
+    assert "__syncthreads();" in s
+    assert "a = a * x1[c];" in s and "a = expf(a);" in s
+
+
+def _compile(src: bytes):
     prog = C.c_void_p()
     assert RTC.hiprtcCreateProgram(C.byref(prog), src, b"plast_chain.hip", 0, None, None) == 0
     opts = [b"--offload-arch=gfx950", b"-O3", b"-std=c++17", b"-ffp-contract=off",
@@ -83,3 +102,17 @@ def test_generated_source_compiles_for_gfx950(case):
     RTC.hiprtcDestroyProgram(C.byref(prog))
     assert rc == 0, log.value.decode(errors="replace")
     assert code.value > 1000
+
+
+@pytest.mark.skipif(RTC is None, reason="libhiprtc not present")
+@pytest.mark.parametrize("case, r", TILE_CASES, ids=[f"{c[0]}-{r:x}" for c, r in TILE_CASES])
+def test_generated_tile_source_compiles_for_gfx950(case, r):
+    name, nin, _, ins = case
+    _compile(source(ins, nin, r, tile=True).encode())
+
+
+@pytest.mark.skipif(RTC is None, reason="libhiprtc not present")
+@pytest.mark.parametrize("case", TAPES, ids=[t[0] for t in TAPES])
+def test_generated_source_compiles_for_gfx950(case):
+    name, nin, bcast, ins = case
+    _compile(source(ins, nin, bcast).encode())

@@ -42,23 +42,24 @@ def _run(rt, ops, tape, devs, jit):
     return out.numpy(), L.plast_hip_chain_jit_launches() - before
 
 
-def _oracle(ins, xs):
-    """The unfused chain, node by node, through the oracle's ops (ones the reference runs)."""
+def _oracle(ins, xs, n=N):
+    """The unfused chain, node by node, through the oracle's ops (ones the reference runs), over n
+    elements (inputs of one element are broadcast scalars)."""
     from hostlib import HostTensor, oracle_forward
     from plast_amd.abi import KernelParams
     n1 = {"NEG": "neg", "EXP": "exp", "LOG": "log", "ABS": "abs", "SIN": "sin", "COS": "cos",
           "TAN": "tan"}
     n2 = {"ADD": "add", "SUB": "sub", "MUL": "mul", "DIV": "div"}
-    full = [np.broadcast_to(x, (N,)).astype(np.float32) for x in xs]
+    full = [np.broadcast_to(x, (n,)).astype(np.float32) for x in xs]
     acc = full[ins[0][2]].copy()
     for op, src, idx, rhs, imm in ins[1:]:
-        out = HostTensor(np.zeros(N, np.float32))
+        out = HostTensor(np.zeros(n, np.float32))
         if op in n1:
             oracle_forward(n1[op], [HostTensor(acc)], out)
         elif op == "LEAKY_RELU":
             oracle_forward("leaky_relu", [HostTensor(acc)], out, KernelParams(0, 0, imm))
         else:
-            o = full[idx] if src == 1 else np.full(N, imm, np.float32) if src == 3 else acc
+            o = full[idx] if src == 1 else np.full(n, imm, np.float32) if src == 3 else acc
             a, b = (o, acc) if rhs else (acc, o)
             oracle_forward(n2[op], [HostTensor(np.ascontiguousarray(a)), HostTensor(np.ascontiguousarray(b))], out)
         acc = out.numpy().copy()
@@ -101,3 +102,77 @@ def test_below_threshold_and_strided_chains_stay_on_the_interpreter():
     before = L.plast_hip_chain_jit_launches()
     ops.fused(tape, small, (4096,))
     assert L.plast_hip_chain_jit_launches() == before
+
+
+# ------------------------------------------------------------------ tile form
+B_, P_, Q_ = 16, 256, 256        # 2^20 outputs of [16, 256, 256], whole 64x64 tiles
+
+
+def _operand(rt, kind, seed):
+    """(device tensor over the output space, host array of the same values as [16, 256, 256])."""
+    rng = np.random.RandomState(seed)
+    if kind == "permuted":           # permute (0, 2, 1) of a contiguous base: staged through LDS
+        base = rng.randn(B_, P_, Q_).astype(np.float32)
+        base[0, 0, :8] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 5.0]
+        d = rt.DeviceTensor.from_numpy(base)
+        v = rt.DeviceTensor((B_, P_, Q_), base=d, strides=(P_ * Q_, 1, Q_), zero=False)
+        return (d, v), base.transpose(0, 2, 1)
+    if kind == "contiguous":         # read directly
+        a = rng.randn(B_, P_, Q_).astype(np.float32)
+        return (rt.DeviceTensor.from_numpy(a),), a
+    if kind == "row":                # [1, P, 1]: one scalar per output row
+        a = rng.uniform(0.5, 1.5, (1, P_, 1)).astype(np.float32)
+        return (rt.DeviceTensor.from_numpy(a),), np.broadcast_to(a, (B_, P_, Q_))
+    a = rng.uniform(0.5, 1.5, (B_, 1, Q_)).astype(np.float32)   # "col": one float4 along p
+    return (rt.DeviceTensor.from_numpy(a),), np.broadcast_to(a, (B_, P_, Q_))
+
+
+TILE_CASES = [
+    (TAPES[0], ["permuted", "row", "col"]),                    # config 3's roles (0, 1, 2)
+    (TAPES[0], ["permuted", "contiguous", "contiguous"]),      # (0, 3, 3)
+    (TAPES[1], ["permuted", "permuted"]),                      # (0, 0): two LDS slots
+    (TAPES[1], ["contiguous", "permuted"]),                    # (3, 0)
+    (TAPES[2], ["permuted"]),                                  # (0)
+    (TAPES[3], ["col", "permuted"]),                           # (2, 0)
+    (TAPES[4], ["permuted", "row", "contiguous", "col"]),      # (0, 1, 3, 2): runtime-role interpreter
+]
+
+
+@pytest.mark.parametrize("case, kinds", TILE_CASES, ids=[f"{c[0]}-{'-'.join(k)}" for c, k in TILE_CASES])
+def test_compiled_tile_matches_interpreter_and_oracle(case, kinds):
+    from gpu_backend import ulp_distance
+    from plast_amd import ops, runtime as rt
+    name, nin, _, ins = case
+    print(f"tile chain {name} {kinds}", flush=True)
+    keep, devs, hosts = [], [], []
+    for k, kind in enumerate(kinds):
+        d, h = _operand(rt, kind, 11 + k)
+        keep.append(d)
+        devs.append(d[-1])
+        hosts.append(np.ascontiguousarray(h).reshape(-1))
+    tape = ops.make_tape(ins, nin)
+    L = rt.lib()
+
+    def run(jit):
+        prev = L.plast_hip_set_chain_jit(1 if jit else 0)
+        before = L.plast_hip_chain_jit_launches()
+        try:
+            out = ops.fused(tape, devs, (B_, P_, Q_))
+            L.check("fused")
+        finally:
+            L.plast_hip_set_chain_jit(prev)
+        return out.numpy().reshape(-1), L.plast_hip_chain_jit_launches() - before
+
+    got, n = run(True)
+    assert n == 1, "the chain did not run compiled"
+    interp, n = run(False)
+    assert n == 0
+    assert_bits(got, interp, f"{name}: compiled tile vs interpreter")
+    inexact = [i for i, (op, *_) in enumerate(ins) if op in ("EXP", "LOG", "SIN", "COS", "TAN")]
+    if inexact and inexact != [len(ins) - 1]:
+        return
+    want = _oracle(ins, hosts, B_ * P_ * Q_)
+    if inexact:
+        assert int(np.max(ulp_distance(got, want))) <= 2
+    else:
+        assert_bits(got, want, f"{name}: compiled tile vs oracle")
