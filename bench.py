@@ -220,17 +220,20 @@ class C4(Workload):
     """Config 4: X [65536,4096] row sum/mean/max/argmax; X^T-shaped [4096,65536] axis-0 sum/max."""
 
     def __init__(self, op, axis):
+        """axis 1: per row, 0: over the leading axis, None: the whole tensor (dim == 9)."""
         self.op, self.axis = op, axis
-        self.name = f"config4_{op}_{'rows' if axis == 1 else 'axis0'}"
+        self.name = f"config4_{op}_{ {1: 'rows', 0: 'axis0', None: 'all'}[axis] }"
         n = 65536 * 4096
+        nout = 1 if axis is None else 65536
         self.elems = n
-        self.bytes_per_call = 4 * n + 65536 * (8 if op == "argmax" else 4)
+        self.bytes_per_call = 4 * n + nout * (8 if op == "argmax" else 4)
 
     def setup(self):
-        shape = (65536, 4096) if self.axis == 1 else (4096, 65536)
+        shape = (65536, 4096) if self.axis != 0 else (4096, 65536)
         self.X = DeviceTensor(shape, zero=False).fill_("normal", 42, 0.0, 1.0)
-        self.out = DeviceTensor((65536,), INT64 if self.op == "argmax" else FLOAT32, zero=False)
-        self.p = KernelParams(self.axis, 0, 0.0)
+        nout = 1 if self.axis is None else 65536
+        self.out = DeviceTensor((nout,), INT64 if self.op == "argmax" else FLOAT32, zero=False)
+        self.p = KernelParams(DIM_ALL if self.axis is None else self.axis, 0, 0.0)
 
     def step(self):
         forward(self.op, [self.X], self.out, self.p)
@@ -409,6 +412,7 @@ def detail_workloads():
         "c3f": C3("fused"), "c3a": C3("add"), "c3m": C3("mul"),
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),
         "c4argmax": C4("argmax", 1), "c4csum": C4("sum", 0), "c4cmax": C4("max", 0),
+        "c4asum": C4("sum", None), "c4amax": C4("max", None),
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),

@@ -56,6 +56,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_ROW_UNROLL
 #define PLAST_ROW_UNROLL 4   // float4 loads in flight per lane, row reductions
 #endif
+#ifndef PLAST_ROW_WAVES
+#define PLAST_ROW_WAVES 4096  // row reductions: split rows into ordered segments up to this many waves
+#endif
 #ifndef PLAST_COL_UNROLL
 #define PLAST_COL_UNROLL 4   // rows in flight per lane, leading-axis reductions
 #endif
