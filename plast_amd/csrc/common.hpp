@@ -106,6 +106,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_BWD_XCD
 #define PLAST_CE_BWD_XCD 1
 #endif
+#ifndef PLAST_CE_UNROLL
+#define PLAST_CE_UNROLL 8     // cross-entropy forward: float4 loads in flight per lane
+#endif
+#ifndef PLAST_OPT_UNROLL
+#define PLAST_OPT_UNROLL 1    // optimizer updates: float4 units per lane
+#endif
 #ifndef PLAST_CE_BWD_MODE
 #define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
 #endif

@@ -18,7 +18,7 @@ namespace plast {
 namespace {
 
 constexpr int kGroup = 64;         // tensors per launch (kernel argument block stays under 4 KiB)
-constexpr int kOptUnroll = 1;      // float4 units per lane
+constexpr int kOptUnroll = PLAST_OPT_UNROLL;  // float4 units per lane
 
 enum class Opt { Sgd, Adam, AdamW };
 

@@ -142,7 +142,7 @@ __device__ __forceinline__ float wave_min(float v) {
   return v;
 }
 
-constexpr int kCeUnroll = 8;  // float4 loads in flight per lane
+constexpr int kCeUnroll = PLAST_CE_UNROLL;  // float4 loads in flight per lane
 
 // One wave64 per row, a single read of the row. Each lane keeps an online (max, exp-sum) pair,
 // rescaling its sum when its max grows; the wave merges the pairs. Rows for which the fast
