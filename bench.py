@@ -159,9 +159,11 @@ class C1(Workload):
 
     def __init__(self, part):
         self.part = part
-        self.name = {"fwd": "config1_bias_relu_fwd_fused", "bwd": "config1_grad_b_sum_axis0"}[part]
+        self.name = {"fwd": "config1_bias_relu_fwd_fused", "bwd": "config1_grad_b_sum_axis0",
+                     "graph": "config1_step_fwd_bwd_graph"}[part]
         self.elems = 1024 * 256
-        self.bytes_per_call = (1024 * 256 * 8 + 1024) if part == "fwd" else (1024 * 256 * 4 + 1024)
+        fwd, bwd = 1024 * 256 * 8 + 1024, 1024 * 256 * 4 + 1024
+        self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd}[part]
 
     def setup(self):
         self.X = DeviceTensor((1024, 256), zero=False).fill_("uniform", 42, -1.0, 1.0)
@@ -173,12 +175,37 @@ class C1(Workload):
         self.tape = make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
                                ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
 
+        self.graph = None
+        if self.part == "graph":
+            # the forward and backward ops recorded once and replayed as one graph launch
+            self.eager_step()
+            L = lib()
+            if L.plast_hip_capture_begin() != 0:
+                raise SystemExit("bench.py: graph capture failed")
+            self.eager_step()
+            self.graph = L.plast_hip_capture_end()
+            L.check("capture")
+
+    def eager_step(self):
+        forward("fused_elementwise", [self.X, self.b], self.Y,
+                KernelParams(C.addressof(self.tape), 0, 0.0))
+        forward("sum", [self.gy], self.gb, KernelParams(0, 0, 0.0))
+
     def step(self):
         if self.part == "fwd":
             forward("fused_elementwise", [self.X, self.b], self.Y,
                     KernelParams(C.addressof(self.tape), 0, 0.0))
-        else:
+        elif self.part == "bwd":
             forward("sum", [self.gy], self.gb, KernelParams(0, 0, 0.0))
+        else:
+            if lib().plast_hip_graph_launch(self.graph) != 0:
+                raise SystemExit("bench.py: graph launch failed")
+
+    def free(self):
+        if self.graph:
+            lib().plast_hip_graph_destroy(self.graph)
+            self.graph = None
+        super().free()
 
 
 class C3(Workload):
@@ -407,7 +434,7 @@ class Copy(Workload):
 def detail_workloads():
     return {
         "copy": Copy(),
-        "c1f": C1("fwd"), "c1b": C1("bwd"),
+        "c1f": C1("fwd"), "c1b": C1("bwd"), "c1g": C1("graph"),
         "c2u": C2Fused(False),
         "c3f": C3("fused"), "c3a": C3("add"), "c3m": C3("mul"),
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),

@@ -260,6 +260,20 @@ int plast_hip_init(int device);
 void plast_hip_set_sync(int sync);
 /* Wait for all work queued on the library stream. Returns 0 on success. */
 int plast_hip_synchronize(void);
+/* Graph capture of launch-bound work. Between plast_hip_capture_begin() and
+ * plast_hip_capture_end(), every kernel the library's entry points launch is recorded on its
+ * stream instead of run (no host waits happen in between), and capture_end returns an
+ * instantiated graph (a hipGraphExec_t) that plast_hip_graph_launch() replays with the same
+ * pointers and shapes, reading whatever the buffers hold at replay time; plast_hip_graph_destroy()
+ * frees it. Only device work can be captured: run each op once before capturing so that the
+ * library's workspaces are already sized (a capture that would grow one fails with an error), and
+ * keep host transfers and allocation outside. The library records fills as kernels, never as
+ * memset nodes. Returns 0 / a non-null graph on success. No counterpart in the reference, which
+ * launches and synchronises op by op. */
+int plast_hip_capture_begin(void);
+void *plast_hip_capture_end(void);
+int plast_hip_graph_launch(void *graph);
+void plast_hip_graph_destroy(void *graph);
 /* The library's stream (a hipStream_t), for callers that order their own work against it. */
 void *plast_hip_stream(void);
 /* Number of errors since the last plast_hip_clear_error(), and the most recent message. */

@@ -11,6 +11,7 @@ namespace {
 int g_device = 0;
 bool g_inited = false;
 bool g_sync = true;
+bool g_capturing = false;  // the library stream is recording a graph
 hipStream_t g_stream = nullptr;
 int g_err_count = 0;
 char g_err_msg[512] = "";
@@ -56,7 +57,7 @@ void finish(const char *where) {
     report_error(where, "kernel launch: %s", hipGetErrorString(e));
     return;
   }
-  if (g_sync) {
+  if (g_sync && !g_capturing) {
     e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) report_error(where, "synchronize: %s", hipGetErrorString(e));
   }
@@ -65,6 +66,11 @@ void finish(const char *where) {
 void *workspace(size_t bytes, int slot) {
   if (slot < 0 || slot >= kSlots) return nullptr;
   if (bytes <= g_ws_bytes[slot]) return g_ws[slot];
+  if (g_capturing) {
+    report_error("workspace", "%zu bytes needed while capturing a graph: run the work once before "
+                 "capturing it", bytes);
+    return nullptr;
+  }
   // Work already queued may still read the old buffer.
   if (g_ws[slot]) {
     (void)hipStreamSynchronize(g_stream);
@@ -289,6 +295,64 @@ int plast_hip_init(int device) {
 
 void plast_hip_set_sync(int sync) { g_sync = sync != 0; }
 
+int plast_hip_capture_begin(void) {
+  if (!ensure_init()) return -1;
+  if (g_capturing) {
+    report_error("plast_hip_capture_begin", "a capture is already open");
+    return -1;
+  }
+  const hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    report_error("plast_hip_capture_begin", "%s", hipGetErrorString(e));
+    return -1;
+  }
+  g_capturing = true;
+  return 0;
+}
+
+void *plast_hip_capture_end(void) {
+  if (!ensure_init()) return nullptr;
+  if (!g_capturing) {
+    report_error("plast_hip_capture_end", "no capture is open");
+    return nullptr;
+  }
+  g_capturing = false;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &graph);
+  if (e != hipSuccess || !graph) {
+    report_error("plast_hip_capture_end", "%s", hipGetErrorString(e));
+    return nullptr;
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) {
+    report_error("plast_hip_capture_end", "instantiate: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  return exec;
+}
+
+int plast_hip_graph_launch(void *graph) {
+  if (!ensure_init() || !graph) return -1;
+  if (g_capturing) {
+    report_error("plast_hip_graph_launch", "cannot launch a graph while capturing");
+    return -1;
+  }
+  const int before = g_err_count;
+  const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), g_stream);
+  if (e != hipSuccess) {
+    report_error("plast_hip_graph_launch", "%s", hipGetErrorString(e));
+    return -1;
+  }
+  finish("plast_hip_graph_launch");
+  return g_err_count == before ? 0 : -1;
+}
+
+void plast_hip_graph_destroy(void *graph) {
+  if (graph) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+}
+
 int plast_hip_synchronize(void) {
   if (!ensure_init()) return -1;
   hipError_t e = hipStreamSynchronize(g_stream);
@@ -341,9 +405,15 @@ void arena_free_hip(void *ptr) {
   PLAST_HIP_TRY("arena_free_hip", hipFree(ptr));
 }
 
+// A fill kernel rather than hipMemsetAsync, so a captured graph holds no memset node.
 void arena_memset_hip(void *ptr, int value, u64 size) {
   if (!ensure_init() || size == 0) return;
-  PLAST_HIP_TRY("arena_memset_hip", hipMemsetAsync(ptr, value, size, g_stream));
+  const unsigned char b = static_cast<unsigned char>(value);
+  if (aligned16(ptr) && size % 4 == 0)
+    fill_u32(ptr, size / 4, 0x01010101u * b, "arena_memset_hip");
+  else
+    fill_bytes_kernel<<<gen_blocks(size), kBlock, 0, stream()>>>(static_cast<unsigned char *>(ptr),
+                                                                 size, b);
   finish("arena_memset_hip");
 }
 

@@ -1,0 +1,126 @@
+"""GPU checks of graph capture (plast_hip_capture_begin / capture_end / graph_launch): config 1's
+training step (the fused relu(X + b) chain, then grad_b = Σ_rows grad_Y through the split
+leading-axis reduction and its finalize) captured once and replayed several times, with fresh
+inputs uploaded eagerly between replays, each replay checked bit for bit against the same step
+run eagerly; plus a flat compiled chain (2^20 elements) captured and replayed, and the error paths
+(nested capture, a launch inside a capture, ending a capture that is not open)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from cases import assert_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _rt():
+    from plast_amd import runtime
+    return runtime
+
+
+def _h2d(dev, arr):
+    L = _rt().lib()
+    a = np.ascontiguousarray(arr, np.float32)
+    L.arena_memcpy_h2d_hip(dev.ptr, a.ctypes.data, a.nbytes)
+    L.check("h2d")
+
+
+def test_config1_step_replays_match_eager():
+    from plast_amd import abi, ops
+    from plast_amd.abi import KernelParams
+    rt = _rt()
+    L = rt.lib()
+    print("graph: config 1 step", flush=True)
+    X, b, gy = (rt.DeviceTensor(s, zero=False) for s in ((1024, 256), (256,), (1024, 256)))
+    Y, gb = rt.DeviceTensor((1024, 256), zero=False), rt.DeviceTensor((256,), zero=False)
+    tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
+                          ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
+
+    def step():
+        rt.forward("fused_elementwise", [X, b], Y, KernelParams(C.addressof(tape), 0, 0.0))
+        rt.forward("sum", [gy], gb, KernelParams(0, 0, 0.0))
+
+    rng = np.random.RandomState(1)
+    for t, shape in ((X, (1024, 256)), (b, (256,)), (gy, (1024, 256))):
+        _h2d(t, rng.uniform(-1, 1, shape))
+    step()                                   # sizes the workspaces outside the capture
+    assert L.plast_hip_capture_begin() == 0
+    step()
+    graph = L.plast_hip_capture_end()
+    L.check("capture")
+    assert graph
+    try:
+        for rep in range(5):
+            for t, shape in ((X, (1024, 256)), (b, (256,)), (gy, (1024, 256))):
+                _h2d(t, rng.uniform(-1, 1, shape))
+            assert L.plast_hip_graph_launch(graph) == 0
+            y_g, gb_g = Y.numpy(), gb.numpy()
+            step()                           # the same step, eagerly, on the same inputs
+            assert_bits(y_g, Y.numpy(), f"replay {rep}: relu(X + b)")
+            assert_bits(gb_g, gb.numpy(), f"replay {rep}: grad_b")
+    finally:
+        L.plast_hip_graph_destroy(graph)
+
+
+def test_compiled_chain_replays():
+    from plast_amd import ops
+    rt = _rt()
+    L = rt.lib()
+    print("graph: compiled chain", flush=True)
+    n = 1 << 20
+    tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("MUL", 1, 1, 0, 0.0), ("ADD", 1, 2, 0, 0.0),
+                          ("LEAKY_RELU", 0, 0, 0, 0.0), ("NEG", 0, 0, 0, 0.0),
+                          ("EXP", 0, 0, 0, 0.0)], 3)
+    ins = [rt.DeviceTensor((n,), zero=False) for _ in range(3)]
+    out = rt.DeviceTensor((n,), zero=False)
+    from plast_amd.abi import KernelParams
+
+    def run():
+        rt.forward("fused_elementwise", ins, out, KernelParams(C.addressof(tape), 0, 0.0))
+
+    rng = np.random.RandomState(2)
+    for t in ins:
+        _h2d(t, rng.randn(n))
+    run()                                    # compiles the chain before the capture
+    before = L.plast_hip_chain_jit_launches()
+    assert L.plast_hip_capture_begin() == 0
+    run()
+    graph = L.plast_hip_capture_end()
+    assert graph
+    try:
+        for rep in range(3):
+            for t in ins:
+                _h2d(t, rng.randn(n))
+            assert L.plast_hip_graph_launch(graph) == 0
+            got = out.numpy()
+            run()
+            assert_bits(got, out.numpy(), f"replay {rep}")
+    finally:
+        L.plast_hip_graph_destroy(graph)
+    assert L.plast_hip_chain_jit_launches() > before
+
+
+def test_capture_errors():
+    rt = _rt()
+    L = rt.lib()
+    x = rt.DeviceTensor((1024,), zero=False)
+    y = rt.DeviceTensor((1024,), zero=False)
+    L.plast_hip_clear_error()
+    assert L.plast_hip_capture_begin() == 0
+    graph = None
+    try:
+        assert L.plast_hip_capture_begin() == -1               # nested
+        assert L.plast_hip_graph_launch(C.c_void_p(1)) == -1   # refused before the handle is used
+        assert L.plast_hip_error_count() == 2
+        L.plast_hip_clear_error()
+        rt.forward("neg", [x], y)                              # recorded, not run
+    finally:
+        graph = L.plast_hip_capture_end()
+    assert graph
+    L.plast_hip_graph_destroy(graph)
+    assert L.plast_hip_capture_end() is None                   # nothing open
+    assert L.plast_hip_error_count() == 1
+    L.plast_hip_clear_error()
