@@ -2,7 +2,7 @@
 seconds, otherwise at a reduced leading extent with the same row/column geometry, plus
 size-independent properties at full size.
 
-Tolerances (written here, from the north star): add/mul/relu/max/argmax bit-exact; exp within 2 ulp
+Tolerances (written here): add/mul/relu/max/argmax bit-exact; exp within 2 ulp
 of glibc; sum/mean/log-sum-exp |gpu - oracle| <= 1e-5 * (sum of |terms|)."""
 from __future__ import annotations
 

@@ -1,7 +1,7 @@
 """GPU parity: every case of tests/cases.py through the HIP library versus the oracle on the same
 seeded inputs.
 
-Bars:
+Bars (the path's stated tolerances):
   add/sub/mul/div/neg/abs/relu/max/min/argmax, index math, every backward without a reduction:
       bit-exact (NaN matches NaN);
   exp/log (and sin/cos/tan): within 2 ulp of glibc;
