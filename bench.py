@@ -155,22 +155,27 @@ class C2Fused(Workload):
 
 
 class C1(Workload):
-    """Config 1: Y = relu(X + b), X [1024,256], b [256] ~ U(-1,1); grad_b = sum_0 grad_Y."""
+    """Config 1: Y = relu(X + b), X [1024,256], b [256] ~ U(-1,1); grad_b = sum_0 grad_Y. "big":
+    the same fused chain over [16384, 4096] (a layer of realistic width, through the compiled
+    rows form)."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"fwd": "config1_bias_relu_fwd_fused", "bwd": "config1_grad_b_sum_axis0",
-                     "graph": "config1_step_fwd_bwd_graph"}[part]
-        self.elems = 1024 * 256
-        fwd, bwd = 1024 * 256 * 8 + 1024, 1024 * 256 * 4 + 1024
-        self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd}[part]
+                     "graph": "config1_step_fwd_bwd_graph",
+                     "big": "bias_relu_fused_16384x4096"}[part]
+        self.rows, self.cols = (16384, 4096) if part == "big" else (1024, 256)
+        self.elems = self.rows * self.cols
+        fwd, bwd = self.elems * 8 + self.cols * 4, self.elems * 4 + self.cols * 4
+        self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd, "big": fwd}[part]
 
     def setup(self):
-        self.X = DeviceTensor((1024, 256), zero=False).fill_("uniform", 42, -1.0, 1.0)
-        self.b = DeviceTensor((256,), zero=False).fill_("uniform", 43, -1.0, 1.0)
-        self.gy = DeviceTensor((1024, 256), zero=False).fill_("uniform", 44, -1.0, 1.0)
-        self.Y = DeviceTensor((1024, 256), zero=False)
-        self.gb = DeviceTensor((256,), zero=False)
+        R, Cn = self.rows, self.cols
+        self.X = DeviceTensor((R, Cn), zero=False).fill_("uniform", 42, -1.0, 1.0)
+        self.b = DeviceTensor((Cn,), zero=False).fill_("uniform", 43, -1.0, 1.0)
+        self.gy = DeviceTensor((R, Cn), zero=False).fill_("uniform", 44, -1.0, 1.0)
+        self.Y = DeviceTensor((R, Cn), zero=False)
+        self.gb = DeviceTensor((Cn,), zero=False)
         from plast_amd.ops import make_tape
         self.tape = make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
                                ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
@@ -192,7 +197,7 @@ class C1(Workload):
         forward("sum", [self.gy], self.gb, KernelParams(0, 0, 0.0))
 
     def step(self):
-        if self.part == "fwd":
+        if self.part in ("fwd", "big"):
             forward("fused_elementwise", [self.X, self.b], self.Y,
                     KernelParams(C.addressof(self.tape), 0, 0.0))
         elif self.part == "bwd":
@@ -434,7 +439,7 @@ class Copy(Workload):
 def detail_workloads():
     return {
         "copy": Copy(),
-        "c1f": C1("fwd"), "c1b": C1("bwd"), "c1g": C1("graph"),
+        "c1f": C1("fwd"), "c1b": C1("bwd"), "c1g": C1("graph"), "c1big": C1("big"),
         "c2u": C2Fused(False),
         "c3f": C3("fused"), "c3a": C3("add"), "c3m": C3("mul"),
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),

@@ -8,6 +8,8 @@
 // functions, compiled with the library's flags (contraction off, no packed fp32) — compiles it once
 // per distinct tape and launch form with hiprtc for the device's architecture, and launches it:
 //  - flat form: inputs unit-stride or broadcast scalars, one float4 per lane;
+//  - rows form: rows of float4 units where an input may be re-read for every row (a bias row)
+//    or be one scalar per row, one float4 per lane;
 //  - tile form: the transposed-operand tile of ew_tile_fixed_kernel (64x64 tiles, operand roles
 //    fixed per kernel) with the tape inlined per output row.
 // Immediates are kernel arguments, so tapes that differ only in constants share a kernel. Compiled
@@ -51,6 +53,17 @@
     unsigned long long simd_end;                                                                   \
     float imm[16];                                                                                 \
   };
+#define PLAST_JIT_ROWS_ARGS                                                                        \
+  struct JitRowsArgs {                                                                             \
+    const float *in[4];                                                                            \
+    float *out;                                                                                    \
+    unsigned long long units;                                                                      \
+    unsigned long long simd_end;                                                                   \
+    float imm[16];                                                                                 \
+    long long ist[4];                                                                              \
+    long long ost;                                                                                 \
+    unsigned dm[3];                                                                                \
+  };
 #define PLAST_JIT_STR2(...) #__VA_ARGS__
 #define PLAST_JIT_STR(...) PLAST_JIT_STR2(__VA_ARGS__)
 
@@ -59,12 +72,24 @@ namespace {
 
 PLAST_JIT_FLAT_ARGS
 PLAST_JIT_TILE_ARGS
+PLAST_JIT_ROWS_ARGS
 static_assert(PLAST_TAPE_MAX_INPUTS == 4 && PLAST_TAPE_MAX_INS == 16 && PLAST_MAX_NDIM == 8,
               "the parameter blocks above are written for these limits");
 
 constexpr uint64_t kMinUnits = uint64_t(1) << 18;  // 2^20 elements: below that, compiling costs more
-constexpr int kJitBlock = 256;                     // lanes per workgroup, both forms
+constexpr int kJitBlock = 256;                     // lanes per workgroup, every form
 constexpr int kJitTile = 64, kJitTilePad = 1;      // the interpreter's tile (kTile, kTilePad)
+// Rows form launch shape, measured on a [16384, 4096] bias + relu chain: two float4 units per lane
+// with ordinary stores 6.48 -> 6.76 TB/s (one unit, or nontemporal stores, or XCD numbering slower).
+#ifndef PLAST_JIT_ROWS_UNROLL
+#define PLAST_JIT_ROWS_UNROLL 2     // rows form: float4 units per lane
+#endif
+#ifndef PLAST_JIT_ROWS_NT_STORE
+#define PLAST_JIT_ROWS_NT_STORE 0   // rows form with a re-read input: nontemporal stores
+#endif
+#ifndef PLAST_JIT_ROWS_XCD
+#define PLAST_JIT_ROWS_XCD 0        // rows form with a re-read input: XCD-contiguous workgroups
+#endif
 
 struct Entry {
   hipModule_t mod = nullptr;
@@ -171,6 +196,69 @@ std::string flat_source(const PlastFusedTape &t, uint32_t bcast) {
   s += "  f4 r;\n";
   s += tape_loop(t, "r", "  ");
   s += "  ((f4 *)A.out)[q] = r;\n";
+  s += "}\n";
+  return s;
+}
+
+// Rows form over [rows, inner] (inner a multiple of 4, unit-stride output rows): bits 0-3 of
+// `pattern` mark inputs that are one scalar per row, bits 8-11 inputs re-read for every row (row
+// stride 0); those are read with ordinary loads (the re-read hits in cache), the streamed ones
+// with nontemporal loads, and a launch with a re-read input keeps dispatch order.
+std::string rows_source(const PlastFusedTape &t, uint32_t pattern) {
+  const uint32_t scalar = pattern & 0xfu, reread = (pattern >> 8) & 0xfu;
+  constexpr int U = PLAST_JIT_ROWS_UNROLL;
+  const bool nt_store = reread && PLAST_JIT_ROWS_NT_STORE;
+  const bool xcd = !reread || PLAST_JIT_ROWS_XCD;
+  std::string s = kPrelude + PLAST_JIT_STR(PLAST_JIT_ROWS_ARGS) + "\n";
+  s += "static __device__ __forceinline__ unsigned mdiv(unsigned n, const unsigned *m) {\n"
+       "  const unsigned long long hi = __umulhi(n, m[0]);\n"
+       "  return (unsigned)((hi + n) >> m[1]);\n"
+       "}\n";
+  s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(kJitBlock) +
+       ") void plast_chain_rows(JitRowsArgs A) {\n";
+  if (xcd) s += kXcdBlock;
+  else s += "  const unsigned bid = blockIdx.x;\n";
+  for (int u = 0; u < U; ++u) {
+    const std::string q = "q" + std::to_string(u), row = "row" + std::to_string(u),
+                      col = "col" + std::to_string(u);
+    s += "  const unsigned " + q + " = bid * " + std::to_string(kJitBlock * U) + " + " +
+         std::to_string(u * kJitBlock) + " + threadIdx.x;\n";
+    s += "  const bool ok" + std::to_string(u) + " = " + q + " < A.units;\n";
+    s += "  const unsigned " + row + " = mdiv(" + q + ", A.dm);\n";
+    s += "  const long long " + col + " = (long long)(" + q + " - " + row + " * A.dm[2]) * 4;\n";
+  }
+  // every load of every unit first, then the chains, then the stores
+  for (int u = 0; u < U; ++u) {
+    const std::string us = std::to_string(u), row = "row" + us, col = "col" + us;
+    for (uint32_t k = 0; k < t.num_inputs; ++k) {
+      const std::string K = std::to_string(k), X = "x" + K + "_" + us;
+      const std::string at = "A.in[" + K + "] + (long long)" + row + " * A.ist[" + K + "]";
+      s += "  f4 " + X + " = f4(0.0f);\n";
+      if (scalar >> k & 1u)
+        s += "  if (ok" + us + ") " + X + " = f4(*(" + at + "));\n";
+      else if (reread >> k & 1u)
+        s += "  if (ok" + us + ") " + X + " = *(const f4 *)(" + at + " + " + col + ");\n";
+      else
+        s += "  if (ok" + us + ") " + X + " = __builtin_nontemporal_load((const f4 *)(" + at + " + " +
+             col + "));\n";
+    }
+  }
+  for (int u = 0; u < U; ++u) {
+    const std::string us = std::to_string(u);
+    s += "  if (ok" + us + ") {\n";
+    s += "    const bool simd = (unsigned long long)q" + us + " * 4 < A.simd_end;\n";
+    s += "    (void)simd;\n";
+    for (uint32_t k = 0; k < t.num_inputs; ++k) {
+      const std::string K = std::to_string(k);
+      s += "    const f4 x" + K + " = x" + K + "_" + us + ";\n";
+      s += "    (void)x" + K + ";\n";
+    }
+    s += "    f4 r;\n";
+    s += tape_loop(t, "r", "    ");
+    s += "    f4 *dst = (f4 *)(A.out + (long long)row" + us + " * A.ost + col" + us + ");\n";
+    s += nt_store ? "    __builtin_nontemporal_store(r, dst);\n" : "    *dst = r;\n";
+    s += "  }\n";
+  }
   s += "}\n";
   return s;
 }
@@ -337,8 +425,9 @@ hipFunction_t kernel_for(char form, uint32_t pattern, const PlastFusedTape &t) {
   auto it = g_cache.find(key);
   if (it == g_cache.end()) {
     Entry e;
-    e.ok = form == 'F' ? compile(flat_source(t, pattern), "plast_chain", device, e)
-                       : compile(tile_source(t, pattern), "plast_chain_tile", device, e);
+    if (form == 'F') e.ok = compile(flat_source(t, pattern), "plast_chain", device, e);
+    else if (form == 'R') e.ok = compile(rows_source(t, pattern), "plast_chain_rows", device, e);
+    else e.ok = compile(tile_source(t, pattern), "plast_chain_tile", device, e);
     it = g_cache.emplace(key, e).first;
   }
   return it->second.ok ? it->second.fn : nullptr;
@@ -388,6 +477,32 @@ bool chain_jit_launch(const PlastFusedTape &t, const float *const *in, uint32_t 
   return launch(fn, &a, unsigned(blocks), 0);
 }
 
+bool chain_jit_rows_launch(const PlastFusedTape &t, const float *const *in, const int64_t *ist,
+                           uint32_t scalar, uint32_t reread, float *out, int64_t ost,
+                           uint64_t units, uint32_t inner4, uint64_t simd_end) {
+  if (units < kMinUnits || units >= (uint64_t(1) << 32) || inner4 == 0) return false;
+  const uint64_t per_block = uint64_t(kJitBlock) * PLAST_JIT_ROWS_UNROLL;
+  const uint64_t blocks = (units + per_block - 1) / per_block;
+  if (blocks > max_blocks(kJitBlock)) return false;
+  const hipFunction_t fn = kernel_for('R', (scalar & 0xfu) | (reread & 0xfu) << 8, t);
+  if (!fn) return false;
+  JitRowsArgs a = {};
+  for (uint32_t k = 0; k < t.num_inputs; ++k) {
+    a.in[k] = in[k];
+    a.ist[k] = ist[k];
+  }
+  a.out = out;
+  a.ost = ost;
+  a.units = units;
+  a.simd_end = simd_end;
+  for (uint32_t i = 0; i < t.num_ins; ++i) a.imm[i] = t.ins[i].imm;
+  const MagicDiv m = MagicDiv::make(inner4);
+  a.dm[0] = m.mul;
+  a.dm[1] = m.shift;
+  a.dm[2] = m.d;
+  return launch(fn, &a, unsigned(blocks), 0);
+}
+
 bool chain_jit_tile_launch(const PlastFusedTape &t, const ChainTileGeometry &g, uint32_t roles,
                            uint64_t elements, uint64_t simd_end, unsigned blocks, size_t lds_bytes) {
   if (elements / 4 < kMinUnits) return false;
@@ -430,6 +545,10 @@ u64 plast_hip_chain_jit_launches(void) {
 
 u64 plast_hip_chain_jit_source(const PlastFusedTape *tape, u32 bcast, char *buf, u64 cap) {
   return well_formed(tape) ? copy_out(flat_source(*tape, bcast), buf, cap) : 0;
+}
+
+u64 plast_hip_chain_jit_rows_source(const PlastFusedTape *tape, u32 pattern, char *buf, u64 cap) {
+  return well_formed(tape) ? copy_out(rows_source(*tape, pattern), buf, cap) : 0;
 }
 
 u64 plast_hip_chain_jit_tile_source(const PlastFusedTape *tape, u32 roles, char *buf, u64 cap) {

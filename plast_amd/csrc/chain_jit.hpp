@@ -15,6 +15,13 @@ namespace plast {
 bool chain_jit_launch(const PlastFusedTape &t, const float *const *in, uint32_t bcast, float *out,
                       uint64_t units, uint64_t simd_end);
 
+// The compiled form over [units / inner4, inner4] float4 units (rows form): input k starts row r at
+// in[k] + r * ist[k]; bit k of `scalar` makes it one value per row, bit k of `reread` marks a row
+// stride of 0 (the same row re-read for every row); output rows start at out + r * ost.
+bool chain_jit_rows_launch(const PlastFusedTape &t, const float *const *in, const int64_t *ist,
+                           uint32_t scalar, uint32_t reread, float *out, int64_t ost,
+                           uint64_t units, uint32_t inner4, uint64_t simd_end);
+
 // Where a transposed-operand tile launch reads and writes (the interpreter's TileArgs, with the
 // output's strides at index PLAST_TAPE_MAX_INPUTS and magic divisors as {mul, shift, d}).
 struct ChainTileGeometry {

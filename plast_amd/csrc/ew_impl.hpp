@@ -636,6 +636,14 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
       if (in_ax == 0 && (A.reused & ~A.bcast_inner) == 0 &&
           chain_jit_launch(body.t, A.in, A.bcast_inner, A.out, A.units, body.simd_end))
         return true;
+      // rows with a re-read bias row or per-row scalars: the rows form
+      if (in_ax == 1) {
+        int64_t ist[PLAST_TAPE_MAX_INPUTS] = {};
+        for (int k = 0; k < NIN; ++k) ist[k] = A.ist[k][0];
+        if (chain_jit_rows_launch(body.t, A.in, ist, A.bcast_inner, A.reused & ~A.bcast_inner,
+                                  A.out, A.ost[0], A.units, uint32_t(inner / 4), body.simd_end))
+          return true;
+      }
     }
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
     const bool done = (A.reused & ~A.bcast_inner) != 0 ? launch_vec<Body, true>(A, body, in_ax)

@@ -28,11 +28,13 @@ def _lib():
     return _L[0]
 
 
-def source(ins, nin, pattern, tile=False) -> str:
-    """The flat form's source (pattern: broadcast mask) or the tile form's (pattern: roles)."""
+def source(ins, nin, pattern, tile=False, rows=False) -> str:
+    """The flat form's source (pattern: broadcast mask), the rows form's (pattern: per-row scalar
+    mask | re-read mask << 8) or the tile form's (pattern: roles)."""
     tape = make_tape(ins, nin)
     L = _lib()
-    f = L.plast_hip_chain_jit_tile_source if tile else L.plast_hip_chain_jit_source
+    f = (L.plast_hip_chain_jit_tile_source if tile else
+         L.plast_hip_chain_jit_rows_source if rows else L.plast_hip_chain_jit_source)
     n = f(C.addressof(tape), pattern, None, 0)
     assert n > 0
     buf = C.create_string_buffer(int(n) + 1)
@@ -116,3 +118,25 @@ def test_generated_tile_source_compiles_for_gfx950(case, r):
 def test_generated_source_compiles_for_gfx950(case):
     name, nin, bcast, ins = case
     _compile(source(ins, nin, bcast).encode())
+
+
+# (tape case, per-row scalar mask, re-read mask): a bias row, a per-row scalar, both
+ROWS_CASES = [(TAPES[0], 0b000, 0b010), (TAPES[0], 0b100, 0b010), (TAPES[1], 0b00, 0b01),
+              (TAPES[4], 0b0010, 0b1000)]
+
+
+def test_rows_source_follows_pattern():
+    (name, nin, _, ins), sc, rr = ROWS_CASES[1]
+    s = source(ins, nin, sc | rr << 8, rows=True)
+    assert "x2_0 = f4(*(A.in[2] + (long long)row0 * A.ist[2]));" in s   # per-row scalar
+    assert "x1_0 = *(const f4 *)(A.in[1]" in s                          # re-read row
+    assert "x0_0 = __builtin_nontemporal_load(" in s                    # x0 streams
+    assert "*dst = r;" in s                                             # ordinary stores
+    assert "gridDim.x / 8" not in s                                               # dispatch order
+
+
+@pytest.mark.skipif(RTC is None, reason="libhiprtc not present")
+@pytest.mark.parametrize("case, sc, rr", ROWS_CASES, ids=[f"{c[0]}-{s:x}-{r:x}" for c, s, r in ROWS_CASES])
+def test_generated_rows_source_compiles_for_gfx950(case, sc, rr):
+    name, nin, _, ins = case
+    _compile(source(ins, nin, sc | rr << 8, rows=True).encode())

@@ -176,3 +176,60 @@ def test_compiled_tile_matches_interpreter_and_oracle(case, kinds):
         assert int(np.max(ulp_distance(got, want))) <= 2
     else:
         assert_bits(got, want, f"{name}: compiled tile vs oracle")
+
+
+# ------------------------------------------------------------------ rows form
+ROWS_CASES = [
+    (TAPES[0], (2048, 1024), ["full", "row", "full"]),          # a bias row re-read for every row
+    (TAPES[0], (2047, 1028), ["full", "row", "col"]),           # plus a per-row scalar; NEG tail
+    (TAPES[1], (2048, 1024), ["row", "full"]),
+    (TAPES[4], (2048, 1024), ["full", "col", "full", "row"]),
+]
+
+
+@pytest.mark.parametrize("case, shape, kinds", ROWS_CASES,
+                         ids=[f"{c[0]}-{s[0]}x{s[1]}-{'-'.join(k)}" for c, s, k in ROWS_CASES])
+def test_compiled_rows_match_interpreter_and_oracle(case, shape, kinds):
+    from gpu_backend import ulp_distance
+    from plast_amd import ops, runtime as rt
+    name, nin, _, ins = case
+    R, Cn = shape
+    print(f"rows chain {name} {shape} {kinds}", flush=True)
+    rng = np.random.RandomState(17)
+    hosts, devs = [], []
+    for kind in kinds:
+        if kind == "full":
+            a = (rng.randn(R, Cn) * 2).astype(np.float32)
+            a[0, :6] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40]
+        elif kind == "row":
+            a = rng.uniform(0.5, 1.5, (1, Cn)).astype(np.float32)
+        else:
+            a = rng.uniform(0.5, 1.5, (R, 1)).astype(np.float32)
+        devs.append(rt.DeviceTensor.from_numpy(a))
+        hosts.append(np.ascontiguousarray(np.broadcast_to(a, (R, Cn))).reshape(-1))
+    tape = ops.make_tape(ins, nin)
+    L = rt.lib()
+
+    def run(jit):
+        prev = L.plast_hip_set_chain_jit(1 if jit else 0)
+        before = L.plast_hip_chain_jit_launches()
+        try:
+            out = ops.fused(tape, devs, (R, Cn))
+            L.check("fused")
+        finally:
+            L.plast_hip_set_chain_jit(prev)
+        return out.numpy().reshape(-1), L.plast_hip_chain_jit_launches() - before
+
+    got, n = run(True)
+    assert n == 1, "the chain did not run compiled"
+    interp, n = run(False)
+    assert n == 0
+    assert_bits(got, interp, f"{name}: compiled rows vs interpreter")
+    inexact = [i for i, (op, *_) in enumerate(ins) if op in ("EXP", "LOG", "SIN", "COS", "TAN")]
+    if inexact and inexact != [len(ins) - 1]:
+        return
+    want = _oracle(ins, hosts, R * Cn)
+    if inexact:
+        assert int(np.max(ulp_distance(got, want))) <= 2
+    else:
+        assert_bits(got, want, f"{name}: compiled rows vs oracle")
