@@ -233,3 +233,41 @@ def test_compiled_rows_match_interpreter_and_oracle(case, shape, kinds):
         assert int(np.max(ulp_distance(got, want))) <= 2
     else:
         assert_bits(got, want, f"{name}: compiled rows vs oracle")
+
+
+def test_compiled_rows_into_a_strided_output_view():
+    """The output is a column slice of a wider tensor (rows padded to 1280 floats): the rows form
+    writes through the output's row stride and leaves the padding alone, and since the output is
+    not contiguous the NEG rule takes its tail form (-x) everywhere, as the interpreter does."""
+    from plast_amd import ops, runtime as rt
+    L = rt.lib()
+    R, Cn, W, off = 2048, 1024, 1280, 128
+    print("rows chain into a strided view", flush=True)
+    rng = np.random.RandomState(23)
+    x = rng.randn(R, Cn).astype(np.float32)
+    x[0, :4] = [0.0, -0.0, 1.0, -1.0]
+    b = rng.uniform(-1, 1, (1, Cn)).astype(np.float32)
+    tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", 1, 1, 0, 0.0), ("NEG", 0, 0, 0, 0.0),
+                          ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
+    dx, db = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(b)
+    results = []
+    for jit in (1, 0):
+        base = rt.DeviceTensor.from_numpy(np.full((R, W), 7.0, np.float32))
+        view = rt.DeviceTensor((R, Cn), base=base, strides=(W, 1), offset=off, zero=False)
+        prev = L.plast_hip_set_chain_jit(jit)
+        before = L.plast_hip_chain_jit_launches()
+        try:
+            from plast_amd.abi import KernelParams
+            import ctypes as C
+            rt.forward("fused_elementwise", [dx, db], view, KernelParams(C.addressof(tape), 0, 0.0))
+        finally:
+            L.plast_hip_set_chain_jit(prev)
+        assert L.plast_hip_chain_jit_launches() - before == jit
+        results.append(base.numpy())
+    got, interp = results
+    assert_bits(got, interp, "compiled rows into a view vs interpreter")
+    assert (got[:, :off] == 7.0).all() and (got[:, off + Cn:] == 7.0).all(), "padding overwritten"
+    s = (x + b).astype(np.float32)
+    want = -s                                     # the tail form of NEG: -x, so -(+0) = -0
+    want = np.where(want > 0, want, want * np.float32(0.0))
+    assert_bits(got[:, off:off + Cn], want, "compiled rows into a view vs closed form")
