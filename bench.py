@@ -58,6 +58,7 @@ class Workload:
     desc = ""
     bytes_per_call = 0
     elems = 0
+    min_steps = 0  # a floor on the timed calls (warm-up: a tenth of it)
 
     def setup(self):
         ...
@@ -165,6 +166,9 @@ class C1(Workload):
                      "graph": "config1_step_fwd_bwd_graph",
                      "big": "bias_relu_fused_16384x4096"}[part]
         self.rows, self.cols = (16384, 4096) if part == "big" else (1024, 256)
+        # calls of a few microseconds: enough of them that the timed region is not a handful of
+        # host round trips
+        self.min_steps = 0 if part == "big" else 500
         self.elems = self.rows * self.cols
         fwd, bwd = self.elems * 8 + self.cols * 4, self.elems * 4 + self.cols * 4
         self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd, "big": fwd}[part]
@@ -455,6 +459,7 @@ def detail_workloads():
 
 def measure(w: Workload, steps: int, warmup: int) -> dict:
     w.setup()
+    steps, warmup = max(steps, w.min_steps), max(warmup, w.min_steps // 10)
     ms = timed(w.step, steps, warmup)
     gbs = w.bytes_per_call / (ms * 1e-3) / 1e9
     r = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
