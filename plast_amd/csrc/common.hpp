@@ -81,8 +81,17 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_COPY_NT_STORE
 #define PLAST_COPY_NT_STORE 0
 #endif
-#ifndef PLAST_OPT_XCD
-#define PLAST_OPT_XCD 1      // optimizer launches holding one tensor entry
+#ifndef PLAST_SGD_XCD
+#define PLAST_SGD_XCD 1      // SGD launches holding one tensor entry
+#endif
+#ifndef PLAST_ADAM_XCD
+#define PLAST_ADAM_XCD 0     // Adam/AdamW launches holding one tensor entry
+#endif
+#ifndef PLAST_SGD_BLOCK
+#define PLAST_SGD_BLOCK 256  // optimizer workgroup sizes
+#endif
+#ifndef PLAST_ADAM_BLOCK
+#define PLAST_ADAM_BLOCK 64
 #endif
 #ifndef PLAST_ADAM_NT_LOAD
 #define PLAST_ADAM_NT_LOAD 1  // Adam/AdamW parameter and moment loads
@@ -98,8 +107,8 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 // XCD-contiguous workgroup numbering elsewhere, measured (4 alternating runs each): row and
 // leading-axis reductions lose 3-12% with it (off); the flat cross-entropy backward gains 2.8% when
-// accumulating (on); a single-tensor Adam/AdamW launch gains about 3% while a launch over many
-// tensors loses 19% (on for one-entry launches only).
+// accumulating (on); a single-tensor SGD launch gains with it, a launch over many tensors loses
+// (on for one-entry launches only); Adam/AdamW with 64-lane workgroups lose 3% with it (off).
 #ifndef PLAST_RED_XCD
 #define PLAST_RED_XCD 0
 #endif

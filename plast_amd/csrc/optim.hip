@@ -22,6 +22,15 @@ constexpr int kOptUnroll = PLAST_OPT_UNROLL;  // float4 units per lane
 
 enum class Opt { Sgd, Adam, AdamW };
 
+// Workgroup size and XCD numbering per update, measured on MI355X over one 64M parameter with its
+// buffers at several relative placements: Adam's seven streams run at 6.30-6.34 TB/s with 64-lane
+// workgroups in dispatch order, against 5.6-6.1 TB/s with 256 lanes and XCD numbering (the larger
+// workgroups were also the ones whose rate moved with placement); SGD keeps 256 lanes, XCD order.
+template <Opt OPT>
+constexpr int kOptBlock = OPT == Opt::Sgd ? PLAST_SGD_BLOCK : PLAST_ADAM_BLOCK;
+template <Opt OPT>
+constexpr bool kOptXcd = (OPT == Opt::Sgd ? PLAST_SGD_XCD : PLAST_ADAM_XCD) != 0;
+
 struct OptArgs {
   float *p[kGroup];
   const float *g[kGroup];
@@ -64,20 +73,26 @@ __device__ __forceinline__ f4 ld(const float *p) {
 
 // XCD: XCD-contiguous workgroup numbering (used for launches holding one tensor entry).
 template <Opt OPT, bool XCD>
-__global__ __launch_bounds__(kBlock) void opt_kernel(OptArgs A) {
+__global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
   constexpr bool kMoments = OPT != Opt::Sgd;
+  constexpr int kBs = kOptBlock<OPT>;
   const uint32_t b = XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
-  int i = 0;
-  while (i + 1 < A.count && b >= A.first_block[i + 1]) ++i;  // uniform
+  // the last entry whose first workgroup is at or before b (uniform binary search)
+  int i = 0, hi = A.count - 1;
+  while (i < hi) {
+    const int mid = (i + hi + 1) >> 1;
+    if (A.first_block[mid] <= b) i = mid;
+    else hi = mid - 1;
+  }
   const uint64_t n = A.n[i];
   float *P = A.p[i];
   const float *G = A.g[i];
   float *M = kMoments ? A.m[i] : nullptr;
   float *V = kMoments ? A.v[i] : nullptr;
-  const uint64_t unit0 = uint64_t(b - A.first_block[i]) * (kBlock * kOptUnroll) + threadIdx.x;
+  const uint64_t unit0 = uint64_t(b - A.first_block[i]) * (kBs * kOptUnroll) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < kOptUnroll; ++u) {
-    const uint64_t e = (unit0 + uint64_t(u) * kBlock) * 4;
+    const uint64_t e = (unit0 + uint64_t(u) * kBs) * 4;
     if (e >= n) continue;
     if (e + 4 <= n && (A.vec_mask >> i & 1u)) {
       f4 p = ld<kOptNtLoad<OPT>>(P + e);
@@ -125,14 +140,15 @@ bool f32_param(const Tensor *t) { return t && t->grad && t->dtype == FLOAT32 && 
 template <Opt OPT>
 void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int count,
                     const char *where) {
+  constexpr int kBs = kOptBlock<OPT>;
   OptArgs A = base;
   A.count = 0;
   uint32_t blocks = 0;
   auto flush = [&]() {
     if (A.count == 0) return;
     A.first_block[A.count] = blocks;
-    if (PLAST_OPT_XCD && A.count == 1) opt_kernel<OPT, true><<<blocks, kBlock, 0, stream()>>>(A);
-    else opt_kernel<OPT, false><<<blocks, kBlock, 0, stream()>>>(A);
+    if (kOptXcd<OPT> && A.count == 1) opt_kernel<OPT, true><<<blocks, kBs, 0, stream()>>>(A);
+    else opt_kernel<OPT, false><<<blocks, kBs, 0, stream()>>>(A);
     A.count = 0;
     A.vec_mask = 0;
     blocks = 0;
@@ -152,12 +168,12 @@ void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int c
     bool aligned = aligned16(P) && aligned16(G);
     if (m) aligned = aligned && aligned16(M) && aligned16(V);
     // a tensor longer than one launch's grid allows is updated as several entries
-    const uint64_t per_block = uint64_t(kBlock) * kOptUnroll * 4;
-    const uint64_t max_piece = max_blocks(kBlock) / 2 * per_block;
+    const uint64_t per_block = uint64_t(kBs) * kOptUnroll * 4;
+    const uint64_t max_piece = max_blocks(kBs) / 2 * per_block;
     for (uint64_t off = 0; off < n; off += max_piece) {
       const uint64_t len = n - off < max_piece ? n - off : max_piece;
       const uint64_t need = (len + per_block - 1) / per_block;
-      if (need > max_blocks(kBlock) - blocks) flush();
+      if (need > max_blocks(kBs) - blocks) flush();
       const int i = A.count;
       A.p[i] = P + off;
       A.g[i] = G + off;

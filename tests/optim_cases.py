@@ -2,7 +2,8 @@
 
 A case is a list of parameter shapes plus a seed; every step draws fresh gradients from the seed,
 so all backends see identical bytes. Shapes cover the float4 body, scalar tails (numel % 4 != 0),
-tiny tensors and more tensors than one launch groups (32).
+tiny tensors, a 40-tensor set (the golden vectors' "many") and more tensors than one launch
+groups (64).
 """
 from __future__ import annotations
 
@@ -13,7 +14,8 @@ import numpy as np
 from plast_amd import abi
 
 SIZES = [(1,), (3,), (4,), (5,), (7, 5), (1000,), (4099,), (64, 33), (2, 3, 4)]
-MANY = [(17,)] * 20 + [(260,)] * 20  # 40 tensors: two launch groups
+MANY = [(17,)] * 20 + [(260,)] * 20  # 40 tensors
+OVER = [(17,)] * 40 + [(260,)] * 40 + [(4099,)] * 3  # 83 tensors: two launch groups
 
 HYPER = {
     "sgd": dict(lr=0.05),

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from cases import assert_bits
-from optim_cases import MANY, SIZES, grads, initial, make_opt
+from optim_cases import MANY, OVER, SIZES, grads, initial, make_opt
 from plast_amd import abi
 from test_optim import run_host
 
@@ -72,9 +72,9 @@ def _run_device(kind, sizes, seed, steps, with_grad, nulls=()):
 
 
 @pytest.mark.parametrize("kind", ["sgd", "adam", "adamw"])
-@pytest.mark.parametrize("set_name", ["shapes", "many"])
+@pytest.mark.parametrize("set_name", ["shapes", "many", "over"])
 def test_gpu_optimizer_matches_oracle(kind, set_name):
-    sizes = SIZES if set_name == "shapes" else MANY
+    sizes = {"shapes": SIZES, "many": MANY, "over": OVER}[set_name]
     print(f"optimizer {kind} {set_name}", flush=True)
     with_grad = [i % 5 != 3 for i in range(len(sizes))]
     po, mvo, _ = run_host("oracle", kind, sizes, 11, 3, with_grad)
