@@ -57,7 +57,11 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #define PLAST_ROW_UNROLL 4   // float4 loads in flight per lane, row reductions
 #endif
 #ifndef PLAST_ROW_WAVES
-#define PLAST_ROW_WAVES 4096  // row reductions: split rows into ordered segments up to this many waves
+// Row reductions: split few long rows into ordered segments up to this many waves. Measured on a
+// whole-tensor sum / max of 2^28 floats (one row): 2048 segments (two workgroups per CU) 6.73 /
+// 6.32 TB/s, 3072 the same, 4096 6.44-6.48 / 6.16 (a longer finalize), 8192 and up 6.05 / 5.79;
+// 1536 and fewer leave CUs idle.
+#define PLAST_ROW_WAVES 2048
 #endif
 #ifndef PLAST_COL_UNROLL
 #define PLAST_COL_UNROLL 4   // rows in flight per lane, leading-axis reductions
@@ -123,6 +127,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 #ifndef PLAST_CE_BWD_MODE
 #define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
+#endif
+#ifndef PLAST_CE_FWD_WAVES
+#define PLAST_CE_FWD_WAVES 4    // cross-entropy forward: rows (one wave each) per workgroup
+#endif
+#ifndef PLAST_CE_BWD_BLOCK
+#define PLAST_CE_BWD_BLOCK 256  // cross-entropy backward, flat form: workgroup size
 #endif
 #ifndef PLAST_CE_BWD_UNROLL
 #define PLAST_CE_BWD_UNROLL 1  // float4 units per lane, cross-entropy backward

@@ -149,13 +149,15 @@ constexpr int kCeUnroll = PLAST_CE_UNROLL;  // float4 loads in flight per lane
 // values could differ from the reference chain's bits (a non-finite logit, a zero or non-finite
 // max, or a shifted-and-normalised logit that overflows to -inf) are recomputed exactly by the
 // same wave from memory.
-__global__ __launch_bounds__(256) void ce_fwd_wave_kernel(const float *__restrict__ x,
+constexpr int kCeFwdWaves = PLAST_CE_FWD_WAVES;  // rows (waves) per workgroup
+
+__global__ __launch_bounds__(64 * kCeFwdWaves) void ce_fwd_wave_kernel(const float *__restrict__ x,
                                                           const int32_t *__restrict__ lab,
                                                           float *__restrict__ stats,
                                                           float *__restrict__ loss, uint64_t N,
                                                           uint32_t C, uint64_t simd_end) {
   const int lane = threadIdx.x & 63;
-  const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const uint64_t row = uint64_t(blockIdx.x) * kCeFwdWaves + (threadIdx.x >> 6);
   if (row >= N) return;  // whole wave
   const float *xr = x + row * C;
   const int32_t y = lab[row];
@@ -278,14 +280,16 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__res
 
 // Backward, float4 path over the flattened [N, C] gradient: one float4 per lane, its row found by
 // magic division; the per-row constants are cached vector loads shared by the wave.
+constexpr int kCeFlatBlock = PLAST_CE_BWD_BLOCK;
+
 template <bool OVERWRITE>
-__global__ __launch_bounds__(kCeBlock) void ce_bwd_flat_kernel(const float *__restrict__ x,
+__global__ __launch_bounds__(kCeFlatBlock) void ce_bwd_flat_kernel(const float *__restrict__ x,
                                                                const int32_t *__restrict__ lab,
                                                                const float *__restrict__ stats,
                                                                const float *__restrict__ dloss,
                                                                float *dx, MagicDiv dc4,
                                                                uint32_t units) {
-  const uint32_t q = (PLAST_CE_BWD_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x) * kCeBlock + threadIdx.x;
+  const uint32_t q = (PLAST_CE_BWD_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x) * kCeFlatBlock + threadIdx.x;
   if (q >= units) return;
   const uint32_t row = dc4.div(q);
   const uint32_t j4 = q - row * dc4.d;
@@ -424,7 +428,8 @@ void softmax_cross_entropy_hip_forward(const Tensor **inputs, Tensor *output, Ke
     float *po = static_cast<float *>(output->data) + r0;
     const uint64_t ser = se > r0 ? se - r0 : 0;  // the rule's boundary, relative to this range
     if (vec)
-      ce_fwd_wave_kernel<<<unsigned(ceil_div(n, 4)), 256, 0, stream()>>>(px, pl, ps, po, n, C, ser);
+      ce_fwd_wave_kernel<<<unsigned(ceil_div(n, kCeFwdWaves)), 64 * kCeFwdWaves, 0, stream()>>>(
+          px, pl, ps, po, n, C, ser);
     else
       ce_fwd_generic_kernel<<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, po, C, ser);
   }
@@ -457,6 +462,8 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
   // rows per launch, so that every grid below stays within the dispatch limit
   uint64_t R = max_blocks(kCeBlock) / chunks;
   if (vec && C4 && R > max_blocks(kCeBlock) * kCeBlock / C4) R = max_blocks(kCeBlock) * kCeBlock / C4;
+  if (vec && C4 && R > max_blocks(kCeFlatBlock) * kCeFlatBlock / C4)
+    R = max_blocks(kCeFlatBlock) * kCeFlatBlock / C4;
   if (R == 0) R = 1;
   for (uint64_t r0 = 0; r0 < N; r0 += R) {
     const uint64_t n = N - r0 < R ? N - r0 : R;
@@ -469,11 +476,11 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
     const uint64_t units = n * C4;
     if (vec && PLAST_CE_BWD_MODE == 1) {
       const MagicDiv dc4 = MagicDiv::make(uint32_t(C4));
-      const unsigned g = unsigned(ceil_div(units, kCeBlock));
+      const unsigned g = unsigned(ceil_div(units, kCeFlatBlock));
       if (over)
-        ce_bwd_flat_kernel<true><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+        ce_bwd_flat_kernel<true><<<g, kCeFlatBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
       else
-        ce_bwd_flat_kernel<false><<<g, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
+        ce_bwd_flat_kernel<false><<<g, kCeFlatBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
     } else if (vec && PLAST_CE_BWD_MODE == 2) {
       if (over) ce_bwd_row_kernel<true><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
       else ce_bwd_row_kernel<false><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);

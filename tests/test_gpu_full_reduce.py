@@ -13,7 +13,7 @@ from cases import assert_bits, assert_sum_parity
 from hostlib import HostTensor, oracle_forward
 
 pytestmark = pytest.mark.gpu
-N = (1 << 24) + 12      # 4096 segments of 4096, the last one ragged
+N = (1 << 24) + 12      # 1986 segments of 8448, the last one ragged
 
 
 def _x(seed, specials):
