@@ -397,16 +397,19 @@ class Pack(Workload):
 
 class Epilogue(Workload):
     """Matmul-epilogue row on a [16384, 4096] output: the leaky-relu gradient modulation
-    dc = dout * (out > 0 ? 1 : alpha) (reads dout, out; writes dc: 12 B/element) and the bias
-    gradient column sum of dc into [4096] (4 B/element + 16 KiB)."""
+    dc = dout * (out > 0 ? 1 : alpha) (reads dout, out; writes dc: 12 B/element), the bias
+    gradient column sum of dc into [4096] (4 B/element + 16 KiB), and both in one pass
+    (12 B/element + 16 KiB: dc is not read back)."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"mod": "epilogue_relu_grad_modulate_16384x4096",
-                     "bias": "epilogue_bias_grad_16384x4096"}[part]
+                     "bias": "epilogue_bias_grad_16384x4096",
+                     "fused": "epilogue_modulate_and_bias_grad_one_pass_16384x4096"}[part]
         self.M, self.N = 16384, 4096
         self.elems = self.M * self.N
-        self.bytes_per_call = self.elems * 12 if part == "mod" else self.elems * 4 + self.N * 4
+        self.bytes_per_call = {"mod": self.elems * 12, "bias": self.elems * 4 + self.N * 4,
+                               "fused": self.elems * 12 + self.N * 4}[part]
 
     def setup(self):
         M, N = self.M, self.N
@@ -420,8 +423,11 @@ class Epilogue(Workload):
         if self.part == "mod":
             L.launch_relu_grad_modulate_hip(self.dout.ptr, self.out.ptr, self.dc.ptr, self.elems,
                                             0.01, 0, 0)
-        else:
+        elif self.part == "bias":
             L.bias_grad_reduce_hip(self.dc.ptr, self.db.ptr, self.elems, self.N)
+        else:
+            L.relu_grad_modulate_bias_grad_hip(self.dout.ptr, self.out.ptr, self.dc.ptr,
+                                               self.db.ptr, self.elems, self.N, 0.01)
 
 
 class Copy(Workload):
@@ -454,6 +460,7 @@ def detail_workloads():
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),
         "epimod": Epilogue("mod"), "epibias": Epilogue("bias"),
+        "epifused": Epilogue("fused"),
     }
 
 

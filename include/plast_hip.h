@@ -167,6 +167,13 @@ void launch_relu_grad_modulate_hip(const float *dout, const float *out_data, flo
  * of cols: the bias-gradient column sum of matmul_bias_relu's backward (src/kernels/cuda/
  * matmul_bias_relu.cu:143-151, 215-220; CPU fused_ops.c:294-304), deterministic (no atomics). */
 void bias_grad_reduce_hip(const float *dc_mod, float *dbias, u64 num_elements, u64 cols);
+/* Both of the above in one call: dc as launch_relu_grad_modulate_hip writes it and dbias as
+ * bias_grad_reduce_hip(dc, ...) writes it, bit for bit, with dout and out_data read once and dc
+ * not read back. Replaces the pair in matmul_bias_relu_cuda_backward (src/kernels/cuda/
+ * matmul_bias_relu.cu:181-186 then 215-220), which writes dc_mod and then re-reads it for the
+ * bias gradient; the reference has no single call for the pair. */
+void relu_grad_modulate_bias_grad_hip(const float *dout, const float *out_data, float *dc,
+                                      float *dbias, u64 num_elements, u64 cols, float alpha);
 
 /* ------------------------------------------------------------------ pack / host transfer ----- */
 

@@ -63,8 +63,17 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // 1536 and fewer leave CUs idle.
 #define PLAST_ROW_WAVES 2048
 #endif
+// Rows in flight per lane, leading-axis reductions, for one-operand and two-operand producers.
+// Measured (two alternating runs): one operand with 2 rather than 4 rows, the axis-0 sum of
+// [4096, 65536] 6.60-6.64 -> 6.72-6.74 TB/s, config 5's bias gradient 6.24-6.26 -> 6.41-6.42, the
+// [16384, 4096] bias gradient 5.24-5.31 -> 5.61-5.64 (1 row loses 11-17% on the first two); two
+// operands (the one-pass relu-gradient modulation and bias sum) 5.38-5.65 with 4 rows, 5.59-5.82
+// with 2, 6.02-6.06 with 1.
 #ifndef PLAST_COL_UNROLL
-#define PLAST_COL_UNROLL 4   // rows in flight per lane, leading-axis reductions
+#define PLAST_COL_UNROLL 2
+#endif
+#ifndef PLAST_COL_UNROLL2
+#define PLAST_COL_UNROLL2 1
 #endif
 #ifndef PLAST_COL_BLOCKS
 #define PLAST_COL_BLOCKS 1024  // workgroups a leading-axis reduction is chunked up to

@@ -28,6 +28,16 @@ namespace plast {
 // ------------------------------------------------------------------------- producers
 // A producer turns the NIN operand values at one point of the space into the reduced value.
 
+// A producer with kStore = true also writes its values out, at operand 0's offsets from its `dst`
+// (the leading-axis kernel only; launch_reduction launches nothing and returns false for any other
+// layout). Producers without the member do not store.
+template <class P, class = void>
+struct StoresValues : std::false_type {};
+template <class P>
+struct StoresValues<P, std::void_t<decltype(P::kStore)>> : std::bool_constant<P::kStore> {};
+template <class P>
+constexpr bool kStores = StoresValues<P>::value;
+
 struct Load1 {
   static constexpr int NIN = 1;
   __device__ __forceinline__ float eval(const float *v) const { return v[0]; }
@@ -37,6 +47,18 @@ struct Load1 {
 struct EqualCount {
   static constexpr int NIN = 2;
   __device__ __forceinline__ float eval(const float *v) const { return v[0] == v[1] ? 1.0f : 0.0f; }
+};
+
+// dout * (z > 0 ? 1 : alpha), stored to dst as it is summed: the relu-gradient modulation of the
+// fused matmul epilogues' backward (matmul_relu.cu:138-144) fused with the bias-gradient sum.
+struct ReluGradStore {
+  static constexpr int NIN = 2;
+  static constexpr bool kStore = true;
+  float alpha;
+  float *dst;
+  __device__ __forceinline__ float eval(const float *v) const {
+    return v[0] * (v[1] > 0.0f ? 1.0f : alpha);
+  }
 };
 
 // ------------------------------------------------------------------------- combiners
@@ -426,7 +448,8 @@ __global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
 
 // ------------------------------------------------------------------------- cols kernel
 
-constexpr int kColUnroll = PLAST_COL_UNROLL;
+template <class Prod>
+constexpr int kColUnroll = Prod::NIN == 1 ? PLAST_COL_UNROLL : PLAST_COL_UNROLL2;
 
 // Fast summary of an order-sensitive fold (exact max/min): the plain extreme and a NaN flag.
 struct ExtFast {
@@ -451,6 +474,7 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   constexpr bool kExt = Comb::kExact;
   constexpr bool IS_MAX = std::is_same<Comb, ExtComb<true>>::value;
   using Fast = typename std::conditional<kExt, ExtFast, Part>::type;
+  static_assert(!(kStores<Prod> && kExt), "a storing producer visits each element once");
   __shared__ Fast sh[kBlock / 64][64 * W];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -477,10 +501,11 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
     if constexpr (kExt) f[c] = Fast{IS_MAX ? -__builtin_huge_valf() : __builtin_huge_valf(), 0u};
     else f[c] = Comb::empty();
   }
-  for (uint64_t r0 = k0 + wv; r0 < k1; r0 += 4 * kColUnroll) {
-    float xv[kColUnroll][NIN][W];
+  constexpr int kU = kColUnroll<Prod>;
+  for (uint64_t r0 = k0 + wv; r0 < k1; r0 += 4 * kU) {
+    float xv[kU][NIN][W];
 #pragma unroll
-    for (int u = 0; u < kColUnroll; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const uint64_t r = r0 + 4 * u;
       if (!active || r >= k1) continue;
 #pragma unroll
@@ -498,21 +523,28 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
       }
     }
 #pragma unroll
-    for (int u = 0; u < kColUnroll; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const uint64_t r = r0 + 4 * u;
       if (!active || r >= k1) continue;
+      float yv[W];
 #pragma unroll
       for (int c = 0; c < W; ++c) {
         float v[NIN];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
         const float y = prod.eval(v);
+        yv[c] = y;
         if constexpr (kExt) {
           f[c].m = IS_MAX ? fmaxf(f[c].m, y) : fminf(f[c].m, y);
           f[c].nan |= y != y ? 1u : 0u;
         } else {
           Comb::next(f[c], y, int64_t(r));
         }
+      }
+      if constexpr (kStores<Prod>) {
+        float *dst = prod.dst + base[0] + int64_t(r) * A.rst[0];
+        if constexpr (VEC) *reinterpret_cast<f4 *>(dst) = f4{yv[0], yv[1], yv[2], yv[3]};
+        else dst[0] = yv[0];
       }
     }
   }
@@ -646,6 +678,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
   s.nops = NIN + 1;
   // An empty space: every output holds the fold of nothing (sum 0, mean 0/0, max -FLT_MAX, ...).
   if (s.numel() == 0) {
+    if constexpr (kStores<Prod>) return false;
     GenArgs<NIN> G;
     memset(&G, 0, sizeof G);
     G.out = out;
@@ -687,7 +720,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
   // ---- rows: single reduced axis, innermost, unit stride for streamed operands
   // one wave per row (segment): the grid is rows * segs / 4 workgroups (rows < 2^32 segments
   // are only split when there are fewer than 4096 rows)
-  if (!empty_space && small_idx && nred == 1 && red_ax == r - 1 &&
+  if (!kStores<Prod> && !empty_space && small_idx && nred == 1 && red_ax == r - 1 &&
       nout <= max_blocks(kBlock) * (kBlock / 64)) {
     RedArgs<NIN> A;
     memset(&A, 0, sizeof A);
@@ -841,6 +874,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
   }
 
   // ---- generic
+  if constexpr (kStores<Prod>) return false;
   GenArgs<NIN> G;
   memset(&G, 0, sizeof G);
   for (int k = 0; k < NIN; ++k) G.in[k] = static_cast<const float *>(in[k]);
