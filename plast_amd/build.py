@@ -2,9 +2,12 @@
 
     python -m plast_amd.build            # library only
     python -m plast_amd.build --oracle   # also oracle/liboracle.so and oracle/_ref (test checker)
+    python -m plast_amd.build -D PLAST_ADAM_BLOCK=256 --out /tmp/adam256.so   # a tuning variant
 
 Objects go to plast_amd/_build/; the shared library is written in-tree so it travels with the
-repository snapshot to the GPU box.
+repository snapshot to the GPU box. A variant (launch-shape knobs of csrc/common.hpp set with -D)
+is built in its own object folder into --out, and is loaded instead of the in-tree library by
+setting PLAST_HIP_LIB to its path.
 """
 from __future__ import annotations
 
@@ -52,30 +55,37 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(err + "\n")
 
 
-def build_library(jobs: int | None = None) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build_library(jobs: int | None = None, defines: list[str] | None = None,
+                  out: Path | None = None) -> Path:
+    defines = list(defines or [])
+    lib = Path(out).resolve() if out else LIB
+    build = BUILD
+    if defines or out:
+        build = PKG / ("_build_" + lib.stem)
+    build.mkdir(exist_ok=True)
+    flags = HIP_FLAGS + [f"-D{d}" for d in defines]
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no sources under {CSRC}")
     cmds = []
     objs = []
     for src in sources:
-        obj = BUILD / (src.stem + ".o")
+        obj = build / (src.stem + ".o")
         objs.append(obj)
         if src.suffix == ".hip":
-            cmds.append([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+            cmds.append([HIPCC, *flags, "-c", str(src), "-o", str(obj)])
         else:
             cmds.append(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{ROOT / 'include'}",
                          "-c", str(src), "-o", str(obj)])
     jobs = jobs or min(len(cmds), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     # hiprtc: the chain compiler (chain_jit.hip)
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
           "-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def build_oracle() -> None:
@@ -88,8 +98,13 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--oracle", action="store_true")
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("-D", dest="defines", action="append", default=[],
+                    help="NAME=VALUE for a launch-shape knob (a variant; needs --out)")
+    ap.add_argument("--out", type=Path, default=None, help="variant library path")
     a = ap.parse_args(argv)
-    print(build_library(a.j))
+    if a.defines and not a.out:
+        ap.error("-D builds a variant: give it --out so the in-tree library stays the default")
+    print(build_library(a.j, a.defines, a.out))
     if a.oracle:
         build_oracle()
     return 0
