@@ -3,7 +3,11 @@
 tanf, in chunks of 2^28) and through the oracle's op, which calls the host's glibc routine as the
 reference's CPU kernels do (unary_ops.c:8-93). Every result must lie within 2 ulp (NaN against NaN
 counts as equal). The host's glibc version is printed with the result. Measured on MI355X against
-glibc 2.35: worst case 1 ulp for exp, 2 ulp for log, sin, cos and tan."""
+glibc 2.35: worst case 1 ulp for exp, 2 ulp for log, sin, cos and tan.
+
+The same sweep runs through a one-instruction fused chain ([LOAD, op]) as well: at 2^28 elements
+the chain is compiled at run time (a separate compilation of the same ocml functions), so this
+pins the compiled chains' math to glibc too, not only to the interpreter."""
 from __future__ import annotations
 
 import concurrent.futures as cf
@@ -29,10 +33,16 @@ def _host_check(name, x, got):
     return float(d[worst]), int((d > 2).sum()), x[worst], got[worst], ho.numpy()[worst]
 
 
+@pytest.mark.parametrize("path", ["op", "chain"])
 @pytest.mark.parametrize("name", ["exp", "log", "sin", "cos", "tan"])
-def test_every_float32_within_2_ulp_of_glibc(name):
-    from plast_amd import runtime as rt
-    print(f"{name}: all 2^32 inputs against {' '.join(platform.libc_ver())}", flush=True)
+def test_every_float32_within_2_ulp_of_glibc(name, path):
+    import ctypes
+    from plast_amd import ops, runtime as rt
+    from plast_amd.abi import KernelParams
+    L = rt.lib()
+    print(f"{name} ({path}): all 2^32 inputs against {' '.join(platform.libc_ver())}", flush=True)
+    tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), (name.upper(), 0, 0, 0, 0.0)], 1)
+    launches = L.plast_hip_chain_jit_launches()
     worst, bad, example = 0.0, 0, None
     base = np.arange(CHUNK, dtype=np.uint32)
     with cf.ThreadPoolExecutor(max_workers=16) as pool:
@@ -40,7 +50,11 @@ def test_every_float32_within_2_ulp_of_glibc(name):
             x = (base + np.uint32(c * CHUNK)).view(np.float32)
             dx = rt.DeviceTensor.from_numpy(x)
             out = rt.DeviceTensor((CHUNK,), zero=False)
-            rt.forward(name, [dx], out)
+            if path == "op":
+                rt.forward(name, [dx], out)
+            else:
+                rt.forward("fused_elementwise", [dx], out,
+                           KernelParams(ctypes.addressof(tape), 0, 0.0))
             got = out.numpy()
             out.free()
             dx.free()
@@ -54,3 +68,5 @@ def test_every_float32_within_2_ulp_of_glibc(name):
             print(f"{name} chunk {c + 1}/16: worst so far {worst:g} ulp, {bad} beyond 2", flush=True)
     assert bad == 0, f"{name}: {bad} inputs beyond 2 ulp; worst {worst:g} ulp at x={example[0]!r}: " \
                      f"gpu {example[1]!r}, glibc {example[2]!r}"
+    if path == "chain":  # every chunk went through the compiled form
+        assert L.plast_hip_chain_jit_launches() - launches == (1 << 32) // CHUNK
