@@ -268,6 +268,40 @@ __device__ ExtPart exact_range(const RedArgs<NIN> &A, const Prod &prod, const in
   return ExtPart{r, kNonEmpty | (last_nan >= 0 ? kIndep : 0u)};
 }
 
+// A parallel-order sum that is not finite (an overflow, or inf - inf) can differ from the
+// reference's serial one, whose outcome depends on the order: such an output is summed again in
+// the reference's order (index order from 0.0f, one rounding per addition: reduce_ops.c:57-61).
+template <class Comb>
+constexpr bool kSerialSum = std::is_same<Comb, SumComb>::value;
+
+__device__ __forceinline__ bool finite_sum(float p) { return fabsf(p) <= FLT_MAX; }
+
+// By one lane: the serial sum of elements [0, len) at base.
+template <class Prod, int NIN>
+__device__ float serial_sum_lane(const RedArgs<NIN> &A, const Prod &prod, const int64_t *base,
+                                 uint64_t len) {
+  float s = 0.0f;
+  for (uint64_t i = 0; i < len; ++i) s = s + value_at(A, prod, base, i);
+  return s;
+}
+
+// By a wave, for a whole row: a NaN operand makes every order's sum NaN, so the wave first looks
+// for one (in parallel) and only a row without one is refolded, by lane 0; every lane returns the
+// result.
+template <class Prod, int NIN>
+__device__ float serial_sum_wave(const RedArgs<NIN> &A, const Prod &prod, const int64_t *base,
+                                 uint64_t len, float p, int lane) {
+  bool nan = false;
+  for (uint64_t i = lane; i < len; i += 64) {
+    const float x = value_at(A, prod, base, i);
+    nan = nan || (x != x);
+  }
+  if (__any(nan)) return p;
+  float r = 0.0f;
+  if (lane == 0) r = serial_sum_lane(A, prod, base, len);
+  return __shfl(r, 0);
+}
+
 constexpr int kRowUnroll = PLAST_ROW_UNROLL;  // float4 loads in flight per lane per operand
 
 template <class Prod, class Comb, bool VEC>
@@ -371,6 +405,9 @@ __global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, 
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) p = Comb::merge(p, Comb::shfl(p, m));
+    // every lane holds the row's sum: the check is uniform over the wave
+    if constexpr (kSerialSum<Comb>)
+      if (A.segs == 1 && !finite_sum(p)) p = serial_sum_wave(A, prod, base, A.len, p, lane);
   }
 
   if (lane != 0) return;
@@ -420,9 +457,10 @@ __device__ __forceinline__ P shfl_down_part(const P &p, int off) {
 // runs merge pairwise, always earlier run on the left (every combiner's merge is associative over
 // ordered ranges; for sums this fixes a different, still deterministic, rounding order than one
 // serial pass). A row of 4096 partials took one thread 50 us to merge serially.
-template <class Comb>
-__global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
+template <class Prod, class Comb>
+__global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<Prod::NIN> A, Prod prod) {
   using Part = typename Comb::Part;
+  constexpr int NIN = Prod::NIN;
   const int lane = threadIdx.x & 63;
   const uint64_t row = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
   if (row >= A.rows) return;  // whole wave
@@ -440,9 +478,13 @@ __global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<1> A) {
     const Part q = shfl_down_part(p, off);
     if ((lane & (2 * off - 1)) == 0 && uint32_t(lane + off) < active) p = Comb::merge(p, q);
   }
-  if (lane != 0) return;
-  int64_t base[1], tbase;
+  int64_t base[NIN], tbase;
   decode_outer(A, uint32_t(row), base, tbase);
+  if constexpr (kSerialSum<Comb>) {
+    p = __shfl(p, 0);  // lane 0 holds the row's sum
+    if (!finite_sum(p)) p = serial_sum_wave(A, prod, base, A.len, p, lane);
+  }
+  if (lane != 0) return;
   store_final<Comb>(A.out, tbase, p, A.post, A.divisor);
 }
 
@@ -583,6 +625,14 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
       p = sh[0][lane * W + c];
 #pragma unroll
       for (int w = 1; w < kBlock / 64; ++w) p = Comb::merge(p, sh[w][lane * W + c]);
+      if constexpr (kSerialSum<Comb>) {
+        if (A.segs == 1 && !finite_sum(p)) {
+          int64_t bc[NIN];
+#pragma unroll
+          for (int k = 0; k < NIN; ++k) bc[k] = base[k] + int64_t(c) * A.kst[k];
+          p = serial_sum_lane(A, prod, bc, A.len);
+        }
+      }
     }
     if (A.segs == 1) {
       store_final<Comb>(A.out, tbase + int64_t(j + c) * A.tkst, p, A.post, A.divisor);
@@ -593,17 +643,25 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   }
 }
 
-template <class Comb>
-__global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<1> A) {
+template <class Prod, class Comb>
+__global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<Prod::NIN> A, Prod prod) {
   using Part = typename Comb::Part;
+  constexpr int NIN = Prod::NIN;
   const uint64_t oi = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
   const uint64_t nout = A.rows * A.inner;
   if (oi >= nout) return;
-  const Part p = merge_in_order<Comb>(static_cast<const Part *>(A.part) + oi, nout, A.segs);
+  Part p = merge_in_order<Comb>(static_cast<const Part *>(A.part) + oi, nout, A.segs);
   const uint32_t o = uint32_t(oi / A.inner);
   const uint64_t j = oi - uint64_t(o) * A.inner;
-  int64_t base[1], tbase;
+  int64_t base[NIN], tbase;
   decode_outer(A, o, base, tbase);
+  if constexpr (kSerialSum<Comb>) {
+    if (!finite_sum(p)) {
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) base[k] += int64_t(j) * A.kst[k];
+      p = serial_sum_lane(A, prod, base, A.len);
+    }
+  }
   store_final<Comb>(A.out, tbase + int64_t(j) * A.tkst, p, A.post, A.divisor);
 }
 
@@ -772,22 +830,9 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
       const unsigned grid = ceil_div(waves, kBlock / 64);
       if (vec) red_rows_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod);
       else red_rows_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod);
-      if (segs > 1) {
-        RedArgs<1> F;
-        memset(&F, 0, sizeof F);
-        F.out = out;
-        F.nouter = A.nouter;
-        for (int d = 0; d < A.nouter; ++d) {
-          F.dv[d] = A.dv[d];
-          F.tst[d] = A.tst[d];
-        }
-        F.rows = A.rows;
-        F.segs = segs;
-        F.part = A.part;
-        F.post = A.post;
-        F.divisor = divisor;
-        red_rows_finalize<Comb><<<ceil_div(A.rows, kBlock / 64), kBlock, 0, stream()>>>(F);
-      }
+      if (segs > 1)  // the finalize reads the partials, and the inputs for a serial refold
+        red_rows_finalize<Prod, Comb>
+            <<<ceil_div(A.rows, kBlock / 64), kBlock, 0, stream()>>>(A, prod);
       return true;
     }
   }
@@ -851,24 +896,8 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
       const dim3 grid{unsigned(base_blocks), unsigned(chunks), 1u};
       if (vec) red_cols_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
       else red_cols_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
-      if (chunks > 1) {
-        RedArgs<1> F;
-        memset(&F, 0, sizeof F);
-        F.out = out;
-        F.nouter = A.nouter;
-        for (int d = 0; d < A.nouter; ++d) {
-          F.dv[d] = A.dv[d];
-          F.tst[d] = A.tst[d];
-        }
-        F.tkst = A.tkst;
-        F.inner = A.inner;
-        F.rows = A.rows;
-        F.segs = A.segs;
-        F.part = A.part;
-        F.post = A.post;
-        F.divisor = divisor;
-        red_cols_finalize<Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(F);
-      }
+      if (chunks > 1)  // the finalize reads the partials, and the inputs for a serial refold
+        red_cols_finalize<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(A, prod);
       return true;
     }
   }

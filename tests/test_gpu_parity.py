@@ -40,6 +40,11 @@ def _reduced_sum(c, x):
 
 @pytest.mark.parametrize("c", CASES, ids=[c.id for c in CASES])
 def test_case(c):
+    check_case(c)
+
+
+def check_case(c):
+    """One case through the HIP library and the oracle, compared at the bars above."""
     from gpu_backend import DeviceBackend, ulp_distance
 
     print(f"case {c.id}", flush=True)
