@@ -1,0 +1,152 @@
+"""Seeded random fused chains: random tapes (2-10 instructions over every op, operand source and
+operand order) over random layouts (flat past the compile threshold, [rows, inner] with a bias row
+and per-row scalars, a transposed operand over whole or partial 64x64 tiles, and a small space
+that stays interpreted). Each chain runs three ways on the GPU and all three must agree bit for
+bit (NaN against NaN):
+  - compiled at run time (where its layout has a compiled form),
+  - on the tape interpreter,
+  - unfused: one library op per instruction (the standalone ops, each pinned to the oracle by
+    tests/test_gpu_parity.py and tests/test_gpu_exhaustive.py), which is the reference's own
+    unfused chain. Both fused forms evaluate each instruction as its op does, with the same
+    rounding and the same ocml functions, so no tolerance is needed even after exp or log.
+Inputs hold signed zeros, infinities, NaN and subnormals."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cases import assert_bits
+from plast_amd.abi import KernelParams, SRC_ACC, SRC_IMM, SRC_INPUT, SRC_NONE
+
+pytestmark = pytest.mark.gpu
+
+UNARY = {"NEG": "neg", "EXP": "exp", "LOG": "log", "ABS": "abs", "SIN": "sin", "COS": "cos",
+         "TAN": "tan", "LEAKY_RELU": "leaky_relu"}
+BINARY = {"ADD": "add", "SUB": "sub", "MUL": "mul", "DIV": "div"}
+
+
+def _tape(rng, nin, first_binary):
+    ins = [("LOAD", SRC_NONE, 0, 0, 0.0)]
+    for j in range(rng.randint(2, 11)):
+        binary = (j == 0 and first_binary) or rng.rand() < 0.55
+        if binary:
+            op = str(rng.choice(list(BINARY)))
+            src = int(rng.choice([SRC_INPUT, SRC_INPUT, SRC_IMM, SRC_ACC]))
+            if j == 0 and first_binary:
+                src = SRC_INPUT
+            idx = int(rng.randint(0, nin)) if src == SRC_INPUT else 0
+            imm = float(np.float32(rng.choice([0.5, -2.5, 3.0, 1e-3, 0.0]))) if src == SRC_IMM else 0.0
+            rhs = int(op in ("SUB", "DIV") and rng.rand() < 0.5)
+            ins.append((op, src, idx, rhs, imm))
+        else:
+            op = str(rng.choice(list(UNARY)))
+            imm = float(np.float32(rng.choice([0.0, 0.01, 0.2]))) if op == "LEAKY_RELU" else 0.0
+            ins.append((op, SRC_NONE, 0, 0, imm))
+    return ins
+
+
+def _values(rng, shape):
+    x = (rng.randn(*shape) * 2).astype(np.float32)
+    flat = x.reshape(-1)
+    pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 88.5, -100.0, 1.0],
+                    np.float32)
+    pick = rng.rand(flat.size) < 0.02
+    flat[pick] = pool[rng.randint(0, len(pool), int(pick.sum()))]
+    return x
+
+
+def _layout(rt, rng, kind, nin):
+    """(device operands, keep-alive list, output shape); operand 0 spans the whole output."""
+    keep = []
+    if kind in ("flat", "small"):
+        n = (1 << 20) + 12 if kind == "flat" else 3000
+        shape = (n,)
+        hs = [_values(rng, shape) if k == 0 or rng.rand() < 0.7 else
+              np.array([rng.uniform(0.5, 2.0)], np.float32) for k in range(nin)]
+        devs = [rt.DeviceTensor.from_numpy(h) for h in hs]
+    elif kind == "rows":
+        R, C = int(rng.choice([1024, 2048])), int(rng.choice([1024, 1028]))
+        shape = (R, C)
+        hs = [_values(rng, shape)]
+        for k in range(1, nin):
+            hs.append([_values(rng, (C,)), rng.uniform(0.5, 2.0, (R, 1)).astype(np.float32),
+                       _values(rng, shape)][rng.randint(0, 3)])
+        devs = [rt.DeviceTensor.from_numpy(h) for h in hs]
+    else:  # tile: operand 0 a permute (0, 2, 1) of a contiguous base
+        B, P, Q = [(16, 256, 256), (3, 130, 200), (4, 128, 192)][rng.randint(0, 3)]
+        shape = (B, P, Q)
+        base = _values(rng, (B, Q, P))
+        d = rt.DeviceTensor.from_numpy(base)
+        keep.append(d)
+        devs = [rt.DeviceTensor(shape, base=d, strides=(P * Q, 1, P), zero=False)]
+        for k in range(1, nin):
+            h = [rng.uniform(0.5, 1.5, (1, P, 1)), rng.uniform(0.5, 1.5, (B, 1, Q)),
+                 _values(rng, shape)][rng.randint(0, 3)].astype(np.float32)
+            devs.append(rt.DeviceTensor.from_numpy(h))
+    return devs, keep, shape
+
+
+def _fused(rt, ops, tape, devs, shape, jit):
+    L = rt.lib()
+    prev = L.plast_hip_set_chain_jit(1 if jit else 0)
+    before = L.plast_hip_chain_jit_launches()
+    try:
+        out = ops.fused(tape, devs, shape)
+        L.check("fused")
+    finally:
+        L.plast_hip_set_chain_jit(prev)
+    return out.numpy(), L.plast_hip_chain_jit_launches() - before
+
+
+def _unfused(rt, ins, devs, shape):
+    acc = devs[0]
+    scalars = []
+    for op, src, idx, rhs, imm in ins[1:]:
+        out = rt.DeviceTensor(shape, zero=False)
+        if op in UNARY:
+            rt.forward(UNARY[op], [acc], out, KernelParams(0, 0, imm))
+        else:
+            if src == SRC_INPUT:
+                o = devs[idx]
+            elif src == SRC_IMM:
+                o = rt.DeviceTensor.from_numpy(np.array([imm], np.float32))
+                scalars.append(o)
+            else:
+                o = acc
+            a, b = (o, acc) if rhs else (acc, o)
+            rt.forward(BINARY[op], [a, b], out)
+        acc = out
+    return acc.numpy()
+
+
+def _cases(n, seed):
+    rng = np.random.RandomState(seed)
+    kinds = ["flat", "rows", "tile", "small"]
+    out = []
+    for i in range(n):
+        kind = kinds[i % 4]
+        nin = int(rng.randint(1, 4))
+        out.append((i, kind, nin, _tape(rng, nin, kind == "tile"), int(rng.randint(1 << 30))))
+    return out
+
+
+CASES = _cases(96, 11)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}_{c[1]}_{c[2]}in_{len(c[3])}ins" for c in CASES])
+def test_random_chain_three_ways(case):
+    from plast_amd import ops, runtime as rt
+    i, kind, nin, ins, seed = case
+    print(f"chain c{i} {kind} {nin} inputs: {[x[0] for x in ins]}", flush=True)
+    rng = np.random.RandomState(seed)
+    devs, keep, shape = _layout(rt, rng, kind, nin)
+    tape = ops.make_tape(ins, nin)
+    compiled, launched = _fused(rt, ops, tape, devs, shape, jit=True)
+    interp, none = _fused(rt, ops, tape, devs, shape, jit=False)
+    assert none == 0
+    if kind == "flat":
+        assert launched == 1, "a flat chain past the threshold did not run compiled"
+    if kind == "small":
+        assert launched == 0
+    assert_bits(compiled, interp, f"c{i}: compiled vs interpreter")
+    assert_bits(interp, _unfused(rt, ins, devs, shape), f"c{i}: fused vs unfused ops")
