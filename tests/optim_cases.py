@@ -29,6 +29,11 @@ def initial(sizes, seed):
     return [rng.randn(*s).astype(np.float32) for s in sizes]
 
 
+SPECIAL_SEED = 66  # grads() for this seed also hold infinities, NaN, subnormals and extremes
+SPECIAL = [(4099,), (260,), (33,)]
+_POOL = np.array([np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3e38, -3e38, 1e-20], np.float32)
+
+
 def grads(sizes, seed, step):
     rng = np.random.RandomState(seed * 1000 + step)
     out = []
@@ -37,6 +42,11 @@ def grads(sizes, seed, step):
         if g.size > 2:
             g.flat[0] = 0.0          # zero gradient: v stays at its decay, sqrt(v) path near 0
             g.flat[1] = -0.0
+        if seed == SPECIAL_SEED:
+            flat = g.reshape(-1)
+            flat[2:2 + min(len(_POOL), flat.size - 2)] = _POOL[:max(0, min(len(_POOL), flat.size - 2))]
+            pick = rng.rand(flat.size) < 0.01
+            flat[pick] = _POOL[rng.randint(0, len(_POOL), int(pick.sum()))]
         out.append(g)
     return out
 

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from cases import assert_bits
-from optim_cases import MANY, OVER, SIZES, grads, initial, make_opt
+from optim_cases import MANY, OVER, SIZES, SPECIAL, SPECIAL_SEED, grads, initial, make_opt
 from plast_amd import abi
 from test_optim import run_host
 
@@ -72,13 +72,14 @@ def _run_device(kind, sizes, seed, steps, with_grad, nulls=()):
 
 
 @pytest.mark.parametrize("kind", ["sgd", "adam", "adamw"])
-@pytest.mark.parametrize("set_name", ["shapes", "many", "over"])
+@pytest.mark.parametrize("set_name", ["shapes", "many", "over", "special_grads"])
 def test_gpu_optimizer_matches_oracle(kind, set_name):
-    sizes = {"shapes": SIZES, "many": MANY, "over": OVER}[set_name]
+    sizes = {"shapes": SIZES, "many": MANY, "over": OVER, "special_grads": SPECIAL}[set_name]
+    seed = SPECIAL_SEED if set_name == "special_grads" else 11
     print(f"optimizer {kind} {set_name}", flush=True)
     with_grad = [i % 5 != 3 for i in range(len(sizes))]
-    po, mvo, _ = run_host("oracle", kind, sizes, 11, 3, with_grad)
-    pd, mvd = _run_device(kind, sizes, 11, 3, with_grad)
+    po, mvo, _ = run_host("oracle", kind, sizes, seed, 3, with_grad)
+    pd, mvd = _run_device(kind, sizes, seed, 3, with_grad)
     for i in range(len(sizes)):
         assert_bits(pd[i], po[i], f"{kind} p{i} {sizes[i]}")
         if mvo is not None:

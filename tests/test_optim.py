@@ -12,7 +12,7 @@ import pytest
 
 from cases import assert_bits
 from hostlib import HostTensor, oracle, ref, ref_available
-from optim_cases import (HYPER, MANY, OVER, SIZES, f64_reference, grads, host_array, initial, make_opt,
+from optim_cases import (HYPER, MANY, OVER, SIZES, SPECIAL, SPECIAL_SEED, f64_reference, grads, host_array, initial, make_opt,
                          read_moments)
 from plast_amd import abi
 
@@ -114,11 +114,12 @@ def run_host(which, kind, sizes, seed, steps, with_grad=None):
 
 @pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built (needs /root/reference)")
 @pytest.mark.parametrize("kind", ["sgd", "adam", "adamw"])
-@pytest.mark.parametrize("sizes", [SIZES, MANY, OVER], ids=["shapes", "many", "over"])
-def test_oracle_optimizer_matches_compiled_reference(kind, sizes):
+@pytest.mark.parametrize("sizes,seed", [(SIZES, 11), (MANY, 11), (OVER, 11), (SPECIAL, SPECIAL_SEED)],
+                         ids=["shapes", "many", "over", "special_grads"])
+def test_oracle_optimizer_matches_compiled_reference(kind, sizes, seed):
     with_grad = [i % 5 != 3 for i in range(len(sizes))]   # some parameters carry no grad
-    po, mvo, _ = run_host("oracle", kind, sizes, 11, 3, with_grad)
-    pr, mvr, _ = run_host("ref", kind, sizes, 11, 3, with_grad)
+    po, mvo, _ = run_host("oracle", kind, sizes, seed, 3, with_grad)
+    pr, mvr, _ = run_host("ref", kind, sizes, seed, 3, with_grad)
     for i, (a, b) in enumerate(zip(po, pr)):
         assert_bits(a, b, f"{kind} param {i}")
     if mvo is not None:
