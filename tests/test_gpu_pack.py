@@ -127,3 +127,54 @@ def test_gpu_pack_config3_size():
     L.hip_tensor_pack_release(C.byref(p))
     want = bdev.numpy().transpose(0, 2, 1)
     assert_bits(got, want, "config-3 pack")
+
+
+def _random_views(n, seed):
+    """Seeded random views of a contiguous base: a slice with steps on each axis, then a
+    permutation of the axes, sometimes with a broadcast (stride 0) axis inserted; sizes reach the
+    whole-tile transposed path (both tile axes of 64 or more)."""
+    rng = np.random.RandomState(seed)
+    out = []
+    for _ in range(n):
+        rank = rng.randint(1, 5)
+        big = rng.rand() < 0.4 and rank >= 2
+        bshape = tuple(int(rng.choice([130, 200, 256])) if big and d >= rank - 2 else
+                       int(rng.randint(1, 12)) for d in range(rank))
+        base = np.arange(int(np.prod(bshape)), dtype=np.int64).reshape(bshape)
+        sl = []
+        for d in bshape:
+            start = int(rng.randint(0, max(1, d // 3)))
+            step = int(rng.choice([1, 1, 1, 2, 3]))
+            sl.append(slice(start, None, step))
+        v = base[tuple(sl)].transpose(rng.permutation(rank))
+        if rng.rand() < 0.3:
+            ax = int(rng.randint(0, v.ndim + 1))
+            v = np.expand_dims(v, ax)
+            shp = list(v.shape)
+            shp[ax] = int(rng.choice([2, 3, 5]))
+            v = np.broadcast_to(v, shp)
+        shape = tuple(int(s) for s in v.shape)
+        strides = tuple(int(s) // 8 for s in v.strides)
+        offset = int((v.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // 8)
+        out.append((bshape, shape, strides, offset))
+    return out
+
+
+RANDOM_VIEWS = _random_views(40, 5)
+
+
+@pytest.mark.parametrize("view", RANDOM_VIEWS, ids=[f"v{i}" for i in range(len(RANDOM_VIEWS))])
+def test_gpu_pack_random_views(view):
+    rt = _rt()
+    L = rt.lib()
+    bshape, shape, strides, off = view
+    print(f"pack {bshape} -> {shape} strides {strides} offset {off}", flush=True)
+    base = _base(bshape, FLOAT32, 9)
+    bdev = rt.DeviceTensor.from_numpy(base)
+    v = _view(rt, bdev, shape, strides, off, FLOAT32)
+    p = abi.HipTensorPack()
+    L.hip_tensor_pack_init(C.byref(p), C.byref(v.t))
+    L.check("hip_tensor_pack_init")
+    assert_bits(_read(p.data, shape, FLOAT32), gather(base, shape, strides, off), "pack")
+    L.hip_tensor_pack_release(C.byref(p))
+    L.check("hip_tensor_pack_release")
