@@ -17,8 +17,8 @@
  * headers and static_asserts equal sizeof/offsetof for every field.
  *
  * Extensions (appended after the reference's last enumerator so every existing numeric value is
- * unchanged): DTYPE gains INT64 (argmax indices); OP_TYPE gains ARGMAX, FUSED_ELEMENTWISE and
- * SOFTMAX_CROSS_ENTROPY.
+ * unchanged): DTYPE gains INT64 (argmax indices); OP_TYPE gains ARGMAX, FUSED_ELEMENTWISE,
+ * SOFTMAX_CROSS_ENTROPY, SOFTMAX and LOG_SOFTMAX.
  */
 #ifndef PLAST_ABI_H
 #define PLAST_ABI_H
@@ -119,6 +119,8 @@ typedef enum OP_TYPE {
   ARGMAX,
   FUSED_ELEMENTWISE,
   SOFTMAX_CROSS_ENTROPY,
+  SOFTMAX,
+  LOG_SOFTMAX,
   PLAST_NUM_OP_TYPES
 } OP_TYPE;
 

@@ -85,6 +85,14 @@ PLAST_HIP_KERNEL_PAIR(fused_elementwise)
  * logits->grad += dloss[i] * (softmax - onehot). */
 PLAST_HIP_KERNEL_PAIR(softmax_cross_entropy)
 
+/* Softmax / log-softmax over the last axis: no reference op; each replaces the op chain of
+ * plast/nn/functional.py:75-97 (MAX(dim, keepdim) -> SUB -> EXP -> SUM(dim, keepdim) -> DIV, or
+ * -> LOG -> SUB). inputs: [0] x, contiguous fp32; output: y, contiguous fp32 of x's shape;
+ * params.dim: the last axis (x->ndim - 1), any other is an error. Backward reads y and y's grad:
+ * x->grad += y * (dy - sum(dy * y)) (softmax) or dy - exp(y) * sum(dy) (log-softmax), per row. */
+PLAST_HIP_KERNEL_PAIR(softmax)
+PLAST_HIP_KERNEL_PAIR(log_softmax)
+
 #undef PLAST_HIP_KERNEL_PAIR
 
 /* ------------------------------------------------------------------ fused-chain tape --------- */

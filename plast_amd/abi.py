@@ -21,7 +21,7 @@ OP_NAMES = [
     "ADD", "SUB", "MUL", "DIV", "MATMUL", "LEAKY_RELU", "LOG", "EXP", "ABS", "NEG", "SIN", "COS",
     "TAN", "VIEW", "TRANSPOSE", "UNSQUEEZE", "SQUEEZE", "EXPAND", "FLATTEN", "BROADCAST", "MEAN",
     "MIN", "MAX", "SUM", "CONV2D", "MATMUL_RELU", "MATMUL_BIAS_RELU", "CONV_RELU",
-    "ARGMAX", "FUSED_ELEMENTWISE", "SOFTMAX_CROSS_ENTROPY",
+    "ARGMAX", "FUSED_ELEMENTWISE", "SOFTMAX_CROSS_ENTROPY", "SOFTMAX", "LOG_SOFTMAX",
 ]
 OP = {name: i for i, name in enumerate(OP_NAMES)}
 

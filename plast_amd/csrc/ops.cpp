@@ -44,6 +44,8 @@ Op make_op(OP_TYPE t) {
     SLOT(ARGMAX, argmax)
     SLOT(FUSED_ELEMENTWISE, fused_elementwise)
     SLOT(SOFTMAX_CROSS_ENTROPY, softmax_cross_entropy)
+    SLOT(SOFTMAX, softmax)
+    SLOT(LOG_SOFTMAX, log_softmax)
 #undef SLOT
   default:
     break;  // MATMUL, CONV2D and their fused epilogues have no GPU slot here

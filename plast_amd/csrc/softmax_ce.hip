@@ -1,4 +1,5 @@
-// softmax_ce.hip — fused softmax cross-entropy over the rows of [N, C] logits with int32 labels.
+// softmax_ce.hip — fused softmax cross-entropy over the rows of [N, C] logits with int32 labels,
+// and softmax / log-softmax over the last axis.
 //
 // Forward, per row (the reference chain MAX -> SUB -> EXP -> SUM -> LOG -> SUB -> MUL(onehot) ->
 // SUM -> NEG of src/api/loss.c:97-169, one HBM read):
@@ -395,6 +396,120 @@ bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *
   return true;
 }
 
+// ---- softmax and log-softmax over the last axis. The reference composes them in Python
+// (plast/nn/functional.py:75-97): MAX(dim, keepdim) -> SUB -> EXP -> SUM(dim, keepdim) -> DIV for
+// softmax, -> LOG -> SUB for log-softmax. One workgroup per row: the reference's max (bit-exact),
+// s = sum_j expf(x_j - m) in the block's fixed order (the reference sums serially), then
+// y = expf(x - m) / s or (x - m) - logf(s): every other step is the reference's own operation.
+template <bool LOG>
+__global__ __launch_bounds__(kCeBlock) void softmax_fwd_kernel(const float *__restrict__ x,
+                                                               float *__restrict__ y, uint32_t C) {
+  __shared__ float lds[kCeWaves + 1];
+  const uint64_t row = blockIdx.x;
+  const float *xr = x + row * C;
+  float *yr = y + row * C;
+  float m = -__builtin_huge_valf();
+  bool nan = false;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) {
+    const float v = xr[j];
+    m = fmaxf(m, v);
+    nan = nan || v != v;
+  }
+  const float mx = row_max_exact(m, nan, xr, C, lds);
+  float s = 0.0f;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) s += expf(xr[j] - mx);
+  s = block_sum(s, lds);
+  if constexpr (LOG) {
+    const float l = logf(s);
+    for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) yr[j] = (xr[j] - mx) - l;
+  } else {
+    for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) yr[j] = expf(xr[j] - mx) / s;
+  }
+}
+
+// Backward from the forward output y: dx += y * (dy - sum_j dy_j y_j) (softmax) or
+// dx += dy - expf(y) * sum_j dy_j (log-softmax), the gradient of the reference chain (its MAX
+// branch contributes zero in exact arithmetic); the row sum in the block's fixed order.
+template <bool LOG>
+__global__ __launch_bounds__(kCeBlock) void softmax_bwd_kernel(const float *__restrict__ y,
+                                                               const float *__restrict__ dy,
+                                                               float *dx, uint32_t C) {
+  __shared__ float lds[kCeWaves + 1];
+  const uint64_t row = blockIdx.x;
+  const float *yr = y + row * C, *gr = dy + row * C;
+  float *dr = dx + row * C;
+  float t = 0.0f;
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) t += LOG ? gr[j] : gr[j] * yr[j];
+  t = block_sum(t, lds);
+  for (uint32_t j = threadIdx.x; j < C; j += kCeBlock) {
+    const float g = LOG ? gr[j] - expf(yr[j]) * t : yr[j] * (gr[j] - t);
+    dr[j] = dr[j] + g;
+  }
+}
+
+bool check_softmax(const Tensor *x, const Tensor *y, KernelParams p, const char *where) {
+  if (x->dtype != FLOAT32 || x->ndim < 1 || !contiguous(x)) {
+    report_error(where, "input must be a contiguous fp32 tensor");
+    return false;
+  }
+  if (y->dtype != FLOAT32 || !contiguous(y) || y->ndim != x->ndim || numel(y) != numel(x)) {
+    report_error(where, "output must be a contiguous fp32 tensor shaped like the input");
+    return false;
+  }
+  if (p.dim != x->ndim - 1) {
+    report_error(where, "only the last axis (dim %llu) is supported, got dim %llu",
+                 (unsigned long long)(x->ndim - 1), (unsigned long long)p.dim);
+    return false;
+  }
+  if (x->shape[x->ndim - 1] >= (uint64_t(1) << 31)) {
+    report_error(where, "rows longer than 2^31 elements are not supported");
+    return false;
+  }
+  return true;
+}
+
+template <bool LOG>
+void softmax_forward(const Tensor **inputs, Tensor *output, KernelParams params,
+                     const char *where) {
+  if (!ensure_init()) return;
+  const Tensor *x = inputs[0];
+  if (!check_softmax(x, output, params, where)) return;
+  const uint32_t C = uint32_t(x->shape[x->ndim - 1]);
+  const uint64_t N = C ? numel(x) / C : 0;
+  const uint64_t R = max_blocks(kCeBlock);
+  for (uint64_t r0 = 0; r0 < N; r0 += R) {
+    const uint64_t n = N - r0 < R ? N - r0 : R;
+    softmax_fwd_kernel<LOG><<<unsigned(n), kCeBlock, 0, stream()>>>(
+        static_cast<const float *>(x->data) + r0 * C, static_cast<float *>(output->data) + r0 * C,
+        C);
+  }
+  finish(where);
+}
+
+template <bool LOG>
+void softmax_backward(Tensor **inputs, const Tensor *output, KernelParams params,
+                      const char *where) {
+  if (!ensure_init()) return;
+  Tensor *x = inputs[0];
+  if (!x->requires_grad || !x->grad) return;
+  if (!check_softmax(x, output, params, where)) return;
+  if (!output->grad || !contiguous(output->grad) || !contiguous(x->grad)) {
+    report_error(where, "needs the output gradient and a contiguous input gradient");
+    return;
+  }
+  const uint32_t C = uint32_t(x->shape[x->ndim - 1]);
+  const uint64_t N = C ? numel(x) / C : 0;
+  const uint64_t R = max_blocks(kCeBlock);
+  for (uint64_t r0 = 0; r0 < N; r0 += R) {
+    const uint64_t n = N - r0 < R ? N - r0 : R;
+    softmax_bwd_kernel<LOG><<<unsigned(n), kCeBlock, 0, stream()>>>(
+        static_cast<const float *>(output->data) + r0 * C,
+        static_cast<const float *>(output->grad->data) + r0 * C,
+        static_cast<float *>(x->grad->data) + r0 * C, C);
+  }
+  finish(where);
+}
+
 }  // namespace
 }  // namespace plast
 
@@ -494,6 +609,19 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
       ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   }
   finish(where);
+}
+
+void softmax_hip_forward(const Tensor **inputs, Tensor *output, KernelParams params) {
+  softmax_forward<false>(inputs, output, params, "softmax_hip_forward");
+}
+void softmax_hip_backward(Tensor **inputs, const Tensor *output, KernelParams params) {
+  softmax_backward<false>(inputs, output, params, "softmax_hip_backward");
+}
+void log_softmax_hip_forward(const Tensor **inputs, Tensor *output, KernelParams params) {
+  softmax_forward<true>(inputs, output, params, "log_softmax_hip_forward");
+}
+void log_softmax_hip_backward(Tensor **inputs, const Tensor *output, KernelParams params) {
+  softmax_backward<true>(inputs, output, params, "log_softmax_hip_backward");
 }
 
 }  // extern "C"

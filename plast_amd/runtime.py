@@ -24,7 +24,7 @@ _DT_OF_NP = {np.dtype(np.float32): FLOAT32, np.dtype(np.int32): INT32, np.dtype(
 OP_NAMES = ["add", "sub", "mul", "div", "exp", "log", "neg", "abs", "sin", "cos", "tan",
             "leaky_relu", "sum", "mean", "max", "min", "argmax", "view", "flatten", "squeeze",
             "unsqueeze", "expand", "broadcast", "transpose", "fused_elementwise",
-            "softmax_cross_entropy"]
+            "softmax_cross_entropy", "softmax", "log_softmax"]
 
 
 class PlastHipError(RuntimeError):

@@ -90,7 +90,7 @@ def test_op_table_fills_gpu_slots():
     L = Library()
     for name in ["ADD", "SUB", "MUL", "DIV", "EXP", "LOG", "NEG", "ABS", "LEAKY_RELU", "SUM",
                  "MEAN", "MAX", "MIN", "ARGMAX", "TRANSPOSE", "FUSED_ELEMENTWISE",
-                 "SOFTMAX_CROSS_ENTROPY"]:
+                 "SOFTMAX_CROSS_ENTROPY", "SOFTMAX", "LOG_SOFTMAX"]:
         op = L.plast_hip_get_op_impl(abi.OP[name])
         assert op.gpu_forward and op.gpu_backward and not op.cpu_forward, name
     op = L.plast_hip_get_op_impl(abi.OP["MATMUL"])

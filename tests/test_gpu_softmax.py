@@ -1,0 +1,129 @@
+"""GPU parity of softmax / log-softmax over the last axis (softmax_hip_* / log_softmax_hip_*).
+
+Forward: against the reference's own op chain run through the oracle (plast/nn/functional.py:75-97:
+MAX(dim, keepdim) -> SUB -> EXP -> SUM(dim, keepdim) -> DIV, or -> LOG -> SUB). The max is
+bit-exact; the only other difference is the row sum's order. The GPU's sum is held to 1e-5
+relative of the exact (float64) sum and the oracle's serial fp32 sum over a long row carries an
+error e_row of its own, so softmax must be within (2e-5 + 2 e_row) * |y| (plus expf's 2 ulp) and
+log-softmax within 1e-5 + 2 e_row + 4e-7 * |y| (log s moves by the sum's relative error); NaN
+against NaN.
+Backward: against the closed form in float64 from the same y, x.grad += y * (dy - sum(dy * y)) or
+dy - exp(y) * sum(dy), within 1e-5 of the terms' magnitude per element, accumulated into an
+existing gradient."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from hostlib import HostTensor, oracle_forward
+from plast_amd.abi import KernelParams
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(4, 10), (33, 1000), (8, 32000), (2, 3, 257), (1, 1), (5, 4096), (6, 9)]
+
+
+def _x(shape, seed):
+    rng = np.random.RandomState(seed)
+    x = (rng.randn(*shape) * 3).astype(np.float32)
+    rows = x.reshape(-1, shape[-1])
+    if rows.shape[0] >= 6 and rows.shape[1] >= 4:
+        rows[0, 1] = np.nan                       # NaN row
+        rows[1, :] = -np.inf                      # max is -FLT_MAX: every term 0, y NaN
+        rows[2, 2] = np.inf                       # inf - inf
+        rows[3, :2] = [3e38, -3e38]               # extreme spread: terms underflow
+        rows[4, :] = 0.0                          # ties at zero, both signs
+        rows[4, ::2] = -0.0
+        rows[5, 0] = 1e-40                        # subnormal
+    return x
+
+
+def _oracle(x, log):
+    C = x.shape[-1]
+    rows = x.reshape(-1, C)
+    R = rows.shape[0]
+
+    def t(a):
+        return HostTensor(np.ascontiguousarray(a, np.float32))
+
+    m = t(np.zeros((R, 1)))
+    oracle_forward("max", [t(rows)], m, KernelParams(1, 1, 0.0))
+    sh = t(np.zeros((R, C)))
+    oracle_forward("sub", [t(rows), m], sh)
+    e = t(np.zeros((R, C)))
+    oracle_forward("exp", [sh], e)
+    s = t(np.zeros((R, 1)))
+    oracle_forward("sum", [e], s, KernelParams(1, 1, 0.0))
+    y = t(np.zeros((R, C)))
+    if log:
+        ls = t(np.zeros((R, 1)))
+        oracle_forward("log", [s], ls)
+        oracle_forward("sub", [sh, ls], y)
+    else:
+        oracle_forward("div", [e, s], y)
+    # the oracle's serial sum against the exact sum of its own terms, per row
+    with np.errstate(invalid="ignore", divide="ignore"):
+        exact = e.numpy().astype(np.float64).sum(1, keepdims=True)
+        err = np.abs(s.numpy().astype(np.float64) - exact) / exact
+    err = np.where(np.isfinite(err), err, 0.0)
+    lead = x.shape[:-1] + (1,)
+    return y.numpy().reshape(x.shape), err.reshape(lead)
+
+
+def _close(got, want, tol, what):
+    both_nan = np.isnan(got) & np.isnan(want)
+    same = (got == want) | both_nan
+    with np.errstate(invalid="ignore"):
+        ok = same | (np.abs(got.astype(np.float64) - want) <= tol)
+    if not ok.all():
+        i = tuple(np.argwhere(~ok)[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} off; first at {i}: "
+                             f"gpu {got[i]!r} want {want[i]!r} tol {np.broadcast_to(tol, got.shape)[i]!r}")
+
+
+@pytest.mark.parametrize("log", [False, True], ids=["softmax", "log_softmax"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[str(s) for s in SHAPES])
+def test_softmax_forward_and_backward(shape, log):
+    from plast_amd import runtime as rt
+    name = "log_softmax" if log else "softmax"
+    print(f"{name} {shape}", flush=True)
+    x = _x(shape, len(shape) * 100 + shape[-1])
+    dx = rt.DeviceTensor.from_numpy(x, requires_grad=True)
+    y = rt.DeviceTensor(shape, requires_grad=True, zero=False)
+    p = KernelParams(len(shape) - 1, 0, 0.0)
+    rt.forward(name, [dx], y, p)
+    got = y.numpy()
+    want, e_row = _oracle(x, log)
+    with np.errstate(invalid="ignore", over="ignore"):
+        tol = ((1e-5 + 2 * e_row + 4e-7 * np.abs(want)) if log else
+               ((2e-5 + 2 * e_row) * np.abs(want) + 1e-37))
+    _close(got, want, tol, f"{name} forward")
+
+    rng = np.random.RandomState(5)
+    dy = rng.randn(*shape).astype(np.float32)
+    prev = rng.randn(*shape).astype(np.float32)
+    L = rt.lib()
+    L.arena_memcpy_h2d_hip(y.grad.ptr, dy.ctypes.data, dy.nbytes)
+    L.arena_memcpy_h2d_hip(dx.grad.ptr, prev.ctypes.data, prev.nbytes)
+    rt.backward(name, [dx], y, p)
+    g = dx.grad.numpy()
+    y64, dy64 = got.astype(np.float64), dy.astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        if log:
+            ey = np.exp(y64)
+            term = dy64 - ey * dy64.sum(-1, keepdims=True)
+            scale = np.abs(dy64) + ey * np.abs(dy64).sum(-1, keepdims=True)
+        else:
+            term = y64 * (dy64 - (dy64 * y64).sum(-1, keepdims=True))
+            scale = np.abs(y64) * (np.abs(dy64) + np.abs(dy64 * y64).sum(-1, keepdims=True))
+        want_g = prev.astype(np.float64) + term
+        tol_g = 1e-5 * scale + 2.4e-7 * np.abs(want_g) + 1e-30
+    _close(g, want_g, tol_g, f"{name} backward")
+
+
+def test_softmax_rejects_other_axes():
+    from plast_amd import runtime as rt
+    x = rt.DeviceTensor.from_numpy(np.ones((3, 4), np.float32))
+    y = rt.DeviceTensor((3, 4), zero=False)
+    with pytest.raises(rt.PlastHipError, match="last axis"):
+        rt.forward("softmax", [x], y, KernelParams(0, 0, 0.0))
