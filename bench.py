@@ -276,17 +276,20 @@ class C4(Workload):
 
 
 class C5(Workload):
-    """Config 5: logits [32768,32000] ~ N(0,2), labels U{0..31999}: CE fwd, bwd, bias-grad sum."""
+    """Config 5: logits [32768,32000] ~ N(0,2), labels U{0..31999}: CE fwd, bwd, bias-grad sum; and
+    softmax over the same logits (one read, one write: 8 B/element)."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"fwd": "config5_softmax_ce_fwd", "bwd": "config5_ce_bwd_accumulate",
-                     "bwd_w": "config5_ce_bwd_overwrite", "bias": "config5_bias_grad_sum_axis0"}[part]
+                     "bwd_w": "config5_ce_bwd_overwrite", "bias": "config5_bias_grad_sum_axis0",
+                     "softmax": "softmax_last_axis_32768x32000"}[part]
         N, Cn = 32768, 32000
         self.elems = N * Cn
         x = 4 * N * Cn
         self.bytes_per_call = {"fwd": x + 3 * 4 * N, "bwd": 3 * x + 3 * 4 * N,
-                               "bwd_w": 2 * x + 3 * 4 * N, "bias": x + 4 * Cn}[part]
+                               "bwd_w": 2 * x + 3 * 4 * N, "bias": x + 4 * Cn,
+                               "softmax": 2 * x}[part]
 
     def setup(self):
         N, Cn = 32768, 32000
@@ -301,6 +304,8 @@ class C5(Workload):
         if self.part == "bias":
             self.G = DeviceTensor((N, Cn), zero=False).fill_("normal", 46, 0.0, 1e-4)
             self.gb = DeviceTensor((Cn,), zero=False)
+        if self.part == "softmax":
+            self.Y = DeviceTensor((N, Cn), zero=False)
 
     def step(self):
         if self.part == "fwd":
@@ -310,8 +315,10 @@ class C5(Workload):
         elif self.part == "bwd_w":
             backward("softmax_cross_entropy", [self.X, self.lab, self.st], self.loss,
                      KernelParams(0, 1, 0.0))
-        else:
+        elif self.part == "bias":
             forward("sum", [self.G], self.gb, KernelParams(0, 0, 0.0))
+        else:
+            forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
 
 
 class Optim(Workload):
@@ -456,6 +463,7 @@ def detail_workloads():
         "c4argmax": C4("argmax", 1), "c4csum": C4("sum", 0), "c4cmax": C4("max", 0),
         "c4asum": C4("sum", None), "c4amax": C4("max", None),
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
+        "c5softmax": C5("softmax"),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),

@@ -137,6 +137,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_BWD_MODE
 #define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
 #endif
+#ifndef PLAST_SOFTMAX_BLOCK
+#define PLAST_SOFTMAX_BLOCK 256  // softmax rows held in registers: lanes per row
+#endif
 #ifndef PLAST_CE_FWD_WAVES
 #define PLAST_CE_FWD_WAVES 4    // cross-entropy forward: rows (one wave each) per workgroup
 #endif

@@ -39,6 +39,8 @@ __device__ __forceinline__ float exp_le0(float t) {
   return t < -87.0f ? 0.0f : e;
 }
 
+// Block-wide reductions over W waves (lds holds W + 1 floats), combined in wave order.
+template <int W = kCeWaves>
 __device__ __forceinline__ float block_sum(float v, float *lds) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
@@ -47,10 +49,11 @@ __device__ __forceinline__ float block_sum(float v, float *lds) {
   __syncthreads();
   float r = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kCeWaves; ++w) r += lds[w];
+  for (int w = 0; w < W; ++w) r += lds[w];
   return r;
 }
 
+template <int W = kCeWaves>
 __device__ __forceinline__ float block_fmax(float v, float *lds) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
@@ -59,12 +62,13 @@ __device__ __forceinline__ float block_fmax(float v, float *lds) {
   __syncthreads();
   float r = lds[0];
 #pragma unroll
-  for (int w = 1; w < kCeWaves; ++w) r = fmaxf(r, lds[w]);
+  for (int w = 1; w < W; ++w) r = fmaxf(r, lds[w]);
   return r;
 }
 
+template <int W = kCeWaves>
 __device__ __forceinline__ bool block_any(bool b, float *lds) {
-  return block_sum(b ? 1.0f : 0.0f, lds) > 0.0f;
+  return block_sum<W>(b ? 1.0f : 0.0f, lds) > 0.0f;
 }
 
 // The reference's serial max fold, for rows whose fast-path extreme is ambiguous (NaN or zero).
@@ -76,15 +80,16 @@ __device__ float serial_max_fold(const float *row, uint32_t C) {
 
 // Row max with exact reference bits: fast block fmax + NaN flag; thread 0 refolds serially when
 // the fast value could differ (a NaN in the row, or a zero maximum whose sign depends on order).
+template <int W = kCeWaves>
 __device__ __forceinline__ float row_max_exact(float m, bool nan, const float *row, uint32_t C,
                                                float *lds) {
-  m = block_fmax(m, lds);
-  nan = block_any(nan, lds);
+  m = block_fmax<W>(m, lds);
+  nan = block_any<W>(nan, lds);
   if (nan || m == 0.0f) {
     __syncthreads();
-    if (threadIdx.x == 0) lds[kCeWaves] = serial_max_fold(row, C);
+    if (threadIdx.x == 0) lds[W] = serial_max_fold(row, C);
     __syncthreads();
-    return lds[kCeWaves];
+    return lds[W];
   }
   return m > -FLT_MAX ? m : -FLT_MAX;
 }
@@ -427,6 +432,64 @@ __global__ __launch_bounds__(kCeBlock) void softmax_fwd_kernel(const float *__re
   }
 }
 
+constexpr int kSoftmaxBlock = PLAST_SOFTMAX_BLOCK;
+
+// The same with the row held in registers, for rows of up to BS * 4 * V floats in whole
+// float4 (C % 4 == 0, 16-byte aligned rows): one read and one write per element. Each lane keeps V
+// float4 of the row; lanes past the row hold -inf, which adds exp(-inf) = 0 to no sum (they are
+// masked) and never wins the max. Same operations and order as softmax_fwd_kernel's three passes
+// but the exp-sum's grouping (per lane, then the block's fixed tree).
+template <bool LOG, int V, int BS = kSoftmaxBlock>
+__global__ __launch_bounds__(BS) void softmax_fwd_reg_kernel(const float *__restrict__ x,
+                                                             float *__restrict__ y, uint32_t C) {
+  constexpr int W = BS / 64;
+  __shared__ float lds[W + 1];
+  const uint64_t row = blockIdx.x;
+  const float *xr = x + row * C;
+  const uint32_t C4 = C / 4;
+  const f4 *x4 = reinterpret_cast<const f4 *>(xr);
+  f4 *y4 = reinterpret_cast<f4 *>(y + row * C);
+  const float ninf = -__builtin_huge_valf();
+  f4 v[V];
+  float m = ninf;
+  bool nan = false;
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t q = threadIdx.x + uint32_t(u) * BS;
+    v[u] = q < C4 ? __builtin_nontemporal_load(x4 + q) : f4(ninf);
+  }
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    m = fmaxf(m, fmaxf(fmaxf(v[u][0], v[u][1]), fmaxf(v[u][2], v[u][3])));
+    nan = nan || v[u][0] != v[u][0] || v[u][1] != v[u][1] || v[u][2] != v[u][2] ||
+          v[u][3] != v[u][3];
+  }
+  const float mx = row_max_exact<W>(m, nan, xr, C, lds);
+  float s = 0.0f;
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const bool in = threadIdx.x + uint32_t(u) * BS < C4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float t = v[u][c] - mx;
+      const float e = expf(t);
+      v[u][c] = LOG ? t : e;
+      s += in ? e : 0.0f;
+    }
+  }
+  s = block_sum<W>(s, lds);
+  const float l = LOG ? logf(s) : 0.0f;
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t q = threadIdx.x + uint32_t(u) * BS;
+    if (q >= C4) continue;
+    f4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = LOG ? v[u][c] - l : v[u][c] / s;
+    y4[q] = r;
+  }
+}
+
 // Backward from the forward output y: dx += y * (dy - sum_j dy_j y_j) (softmax) or
 // dx += dy - expf(y) * sum_j dy_j (log-softmax), the gradient of the reference chain (its MAX
 // branch contributes zero in exact arithmetic); the row sum in the block's fixed order.
@@ -477,11 +540,24 @@ void softmax_forward(const Tensor **inputs, Tensor *output, KernelParams params,
   const uint32_t C = uint32_t(x->shape[x->ndim - 1]);
   const uint64_t N = C ? numel(x) / C : 0;
   const uint64_t R = max_blocks(kCeBlock);
+  // float4 units per lane for a register-resident row (0: the three-pass kernel)
+  int V = 0;
+  if (C % 4 == 0 && aligned16(x->data) && aligned16(output->data))
+    for (int v = 1; v <= 32 && !V; v *= 2)
+      if (uint64_t(C) <= uint64_t(kSoftmaxBlock) * 4 * v) V = v;
   for (uint64_t r0 = 0; r0 < N; r0 += R) {
-    const uint64_t n = N - r0 < R ? N - r0 : R;
-    softmax_fwd_kernel<LOG><<<unsigned(n), kCeBlock, 0, stream()>>>(
-        static_cast<const float *>(x->data) + r0 * C, static_cast<float *>(output->data) + r0 * C,
-        C);
+    const unsigned n = unsigned(N - r0 < R ? N - r0 : R);
+    const float *px = static_cast<const float *>(x->data) + r0 * C;
+    float *py = static_cast<float *>(output->data) + r0 * C;
+    switch (V) {
+      case 1: softmax_fwd_reg_kernel<LOG, 1><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      case 2: softmax_fwd_reg_kernel<LOG, 2><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      case 4: softmax_fwd_reg_kernel<LOG, 4><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      case 8: softmax_fwd_reg_kernel<LOG, 8><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      case 16: softmax_fwd_reg_kernel<LOG, 16><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      case 32: softmax_fwd_reg_kernel<LOG, 32><<<n, kSoftmaxBlock, 0, stream()>>>(px, py, C); break;
+      default: softmax_fwd_kernel<LOG><<<n, kCeBlock, 0, stream()>>>(px, py, C); break;
+    }
   }
   finish(where);
 }
