@@ -277,19 +277,21 @@ class C4(Workload):
 
 class C5(Workload):
     """Config 5: logits [32768,32000] ~ N(0,2), labels U{0..31999}: CE fwd, bwd, bias-grad sum; and
-    softmax over the same logits (one read, one write: 8 B/element)."""
+    softmax over the same logits (one read, one write: 8 B/element) and its backward (y, dy and
+    the accumulated dx read, dx written: 16 B/element)."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"fwd": "config5_softmax_ce_fwd", "bwd": "config5_ce_bwd_accumulate",
                      "bwd_w": "config5_ce_bwd_overwrite", "bias": "config5_bias_grad_sum_axis0",
-                     "softmax": "softmax_last_axis_32768x32000"}[part]
+                     "softmax": "softmax_last_axis_32768x32000",
+                     "softmax_bwd": "softmax_backward_last_axis_32768x32000"}[part]
         N, Cn = 32768, 32000
         self.elems = N * Cn
         x = 4 * N * Cn
         self.bytes_per_call = {"fwd": x + 3 * 4 * N, "bwd": 3 * x + 3 * 4 * N,
                                "bwd_w": 2 * x + 3 * 4 * N, "bias": x + 4 * Cn,
-                               "softmax": 2 * x}[part]
+                               "softmax": 2 * x, "softmax_bwd": 4 * x}[part]
 
     def setup(self):
         N, Cn = 32768, 32000
@@ -304,8 +306,13 @@ class C5(Workload):
         if self.part == "bias":
             self.G = DeviceTensor((N, Cn), zero=False).fill_("normal", 46, 0.0, 1e-4)
             self.gb = DeviceTensor((Cn,), zero=False)
-        if self.part == "softmax":
-            self.Y = DeviceTensor((N, Cn), zero=False)
+        if self.part in ("softmax", "softmax_bwd"):
+            self.Y = DeviceTensor((N, Cn), requires_grad=self.part == "softmax_bwd", zero=False)
+        if self.part == "softmax_bwd":
+            self.X = DeviceTensor((N, Cn), FLOAT32, requires_grad=True,
+                                  zero=False).fill_("normal", 42, 0.0, 2.0)
+            forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
+            self.Y.grad.fill_("normal", 47, 0.0, 1.0)
 
     def step(self):
         if self.part == "fwd":
@@ -317,8 +324,10 @@ class C5(Workload):
                      KernelParams(0, 1, 0.0))
         elif self.part == "bias":
             forward("sum", [self.G], self.gb, KernelParams(0, 0, 0.0))
-        else:
+        elif self.part == "softmax":
             forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
+        else:
+            backward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
 
 
 class Optim(Workload):
@@ -463,7 +472,7 @@ def detail_workloads():
         "c4argmax": C4("argmax", 1), "c4csum": C4("sum", 0), "c4cmax": C4("max", 0),
         "c4asum": C4("sum", None), "c4amax": C4("max", None),
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
-        "c5softmax": C5("softmax"),
+        "c5softmax": C5("softmax"), "c5softmaxb": C5("softmax_bwd"),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),

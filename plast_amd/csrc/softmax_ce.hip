@@ -510,6 +510,45 @@ __global__ __launch_bounds__(kCeBlock) void softmax_bwd_kernel(const float *__re
   }
 }
 
+// The backward with y and dy of a row held in registers (rows of whole float4 up to BS * 4 * V
+// floats): y, dy and dx are each read once and dx written once. The sum's grouping is per lane,
+// then the block's fixed tree.
+template <bool LOG, int V, int BS>
+__global__ __launch_bounds__(BS) void softmax_bwd_reg_kernel(const float *__restrict__ y,
+                                                             const float *__restrict__ dy,
+                                                             float *dx, uint32_t C) {
+  constexpr int W = BS / 64;
+  __shared__ float lds[W + 1];
+  const uint64_t row = blockIdx.x;
+  const uint32_t C4 = C / 4;
+  const f4 *y4 = reinterpret_cast<const f4 *>(y + row * C);
+  const f4 *g4 = reinterpret_cast<const f4 *>(dy + row * C);
+  f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
+  f4 yv[V], gv[V];
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t q = threadIdx.x + uint32_t(u) * BS;
+    yv[u] = q < C4 ? __builtin_nontemporal_load(y4 + q) : f4(0.0f);
+    gv[u] = q < C4 ? __builtin_nontemporal_load(g4 + q) : f4(0.0f);
+  }
+  float t = 0.0f;
+#pragma unroll
+  for (int u = 0; u < V; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t += LOG ? gv[u][c] : gv[u][c] * yv[u][c];
+  t = block_sum<W>(t, lds);
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t q = threadIdx.x + uint32_t(u) * BS;
+    if (q >= C4) continue;
+    f4 d = d4[q];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      d[c] = d[c] + (LOG ? gv[u][c] - expf(yv[u][c]) * t : yv[u][c] * (gv[u][c] - t));
+    d4[q] = d;
+  }
+}
+
 bool check_softmax(const Tensor *x, const Tensor *y, KernelParams p, const char *where) {
   if (x->dtype != FLOAT32 || x->ndim < 1 || !contiguous(x)) {
     report_error(where, "input must be a contiguous fp32 tensor");
@@ -576,12 +615,25 @@ void softmax_backward(Tensor **inputs, const Tensor *output, KernelParams params
   const uint32_t C = uint32_t(x->shape[x->ndim - 1]);
   const uint64_t N = C ? numel(x) / C : 0;
   const uint64_t R = max_blocks(kCeBlock);
+  constexpr int BS = 512;  // y and dy in registers: 512 lanes keep V at 16 for 32768-float rows
+  int V = 0;
+  if (C % 4 == 0 && aligned16(output->data) && aligned16(output->grad->data) &&
+      aligned16(x->grad->data))
+    for (int v = 1; v <= 16 && !V; v *= 2)
+      if (uint64_t(C) <= uint64_t(BS) * 4 * v) V = v;
   for (uint64_t r0 = 0; r0 < N; r0 += R) {
-    const uint64_t n = N - r0 < R ? N - r0 : R;
-    softmax_bwd_kernel<LOG><<<unsigned(n), kCeBlock, 0, stream()>>>(
-        static_cast<const float *>(output->data) + r0 * C,
-        static_cast<const float *>(output->grad->data) + r0 * C,
-        static_cast<float *>(x->grad->data) + r0 * C, C);
+    const unsigned n = unsigned(N - r0 < R ? N - r0 : R);
+    const float *py = static_cast<const float *>(output->data) + r0 * C;
+    const float *pg = static_cast<const float *>(output->grad->data) + r0 * C;
+    float *pd = static_cast<float *>(x->grad->data) + r0 * C;
+    switch (V) {
+      case 1: softmax_bwd_reg_kernel<LOG, 1, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      case 2: softmax_bwd_reg_kernel<LOG, 2, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      case 4: softmax_bwd_reg_kernel<LOG, 4, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      case 8: softmax_bwd_reg_kernel<LOG, 8, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      case 16: softmax_bwd_reg_kernel<LOG, 16, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      default: softmax_bwd_kernel<LOG><<<n, kCeBlock, 0, stream()>>>(py, pg, pd, C); break;
+    }
   }
   finish(where);
 }
