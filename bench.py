@@ -295,7 +295,8 @@ class C5(Workload):
 
     def setup(self):
         N, Cn = 32768, 32000
-        self.X = DeviceTensor((N, Cn), FLOAT32, requires_grad=self.part in ("bwd", "bwd_w"),
+        self.X = DeviceTensor((N, Cn), FLOAT32,
+                              requires_grad=self.part in ("bwd", "bwd_w", "softmax_bwd"),
                               zero=False).fill_("normal", 42, 0.0, 2.0)
         self.lab = DeviceTensor((N,), INT32, zero=False).fill_("randint", 45, 0, Cn)
         self.st = DeviceTensor((N, 2), zero=False)
@@ -309,8 +310,6 @@ class C5(Workload):
         if self.part in ("softmax", "softmax_bwd"):
             self.Y = DeviceTensor((N, Cn), requires_grad=self.part == "softmax_bwd", zero=False)
         if self.part == "softmax_bwd":
-            self.X = DeviceTensor((N, Cn), FLOAT32, requires_grad=True,
-                                  zero=False).fill_("normal", 42, 0.0, 2.0)
             forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
             self.Y.grad.fill_("normal", 47, 0.0, 1.0)
 
