@@ -278,20 +278,24 @@ class C4(Workload):
 class C5(Workload):
     """Config 5: logits [32768,32000] ~ N(0,2), labels U{0..31999}: CE fwd, bwd, bias-grad sum; and
     softmax over the same logits (one read, one write: 8 B/element) and its backward (y, dy and
-    the accumulated dx read, dx written: 16 B/element)."""
+    the accumulated dx read, dx written: 16 B/element); and the reference chain's individual ops
+    on the logits: MAX and SUM over dim 1 with keepdim (4 B/element + 4 B/row), EXP (8 B/element)."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"fwd": "config5_softmax_ce_fwd", "bwd": "config5_ce_bwd_accumulate",
                      "bwd_w": "config5_ce_bwd_overwrite", "bias": "config5_bias_grad_sum_axis0",
                      "softmax": "softmax_last_axis_32768x32000",
-                     "softmax_bwd": "softmax_backward_last_axis_32768x32000"}[part]
+                     "softmax_bwd": "softmax_backward_last_axis_32768x32000",
+                     "op_max": "config5_op_max_dim1", "op_exp": "config5_op_exp",
+                     "op_sum": "config5_op_sum_dim1"}[part]
         N, Cn = 32768, 32000
         self.elems = N * Cn
         x = 4 * N * Cn
         self.bytes_per_call = {"fwd": x + 3 * 4 * N, "bwd": 3 * x + 3 * 4 * N,
                                "bwd_w": 2 * x + 3 * 4 * N, "bias": x + 4 * Cn,
-                               "softmax": 2 * x, "softmax_bwd": 4 * x}[part]
+                               "softmax": 2 * x, "softmax_bwd": 4 * x,
+                               "op_max": x + 4 * N, "op_exp": 2 * x, "op_sum": x + 4 * N}[part]
 
     def setup(self):
         N, Cn = 32768, 32000
@@ -312,6 +316,10 @@ class C5(Workload):
         if self.part == "softmax_bwd":
             forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
             self.Y.grad.fill_("normal", 47, 0.0, 1.0)
+        if self.part in ("op_max", "op_sum"):
+            self.R = DeviceTensor((N, 1), zero=False)
+        if self.part == "op_exp":
+            self.Y = DeviceTensor((N, Cn), zero=False)
 
     def step(self):
         if self.part == "fwd":
@@ -325,6 +333,10 @@ class C5(Workload):
             forward("sum", [self.G], self.gb, KernelParams(0, 0, 0.0))
         elif self.part == "softmax":
             forward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
+        elif self.part in ("op_max", "op_sum"):
+            forward(self.part[3:], [self.X], self.R, KernelParams(1, 1, 0.0))
+        elif self.part == "op_exp":
+            forward("exp", [self.X], self.Y)
         else:
             backward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
 
@@ -472,6 +484,7 @@ def detail_workloads():
         "c4asum": C4("sum", None), "c4amax": C4("max", None),
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
         "c5softmax": C5("softmax"), "c5softmaxb": C5("softmax_bwd"),
+        "c5max": C5("op_max"), "c5exp": C5("op_exp"), "c5sum": C5("op_sum"),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),
