@@ -777,7 +777,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
 
   // ---- rows: single reduced axis, innermost, unit stride for streamed operands
   // one wave per row (segment): the grid is rows * segs / 4 workgroups (rows < 2^32 segments
-  // are only split when there are fewer than 4096 rows)
+  // are only split when there are fewer than PLAST_ROW_WAVES rows)
   if (!kStores<Prod> && !empty_space && small_idx && nred == 1 && red_ax == r - 1 &&
       nout <= max_blocks(kBlock) * (kBlock / 64)) {
     RedArgs<NIN> A;
