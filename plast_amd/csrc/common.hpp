@@ -75,6 +75,13 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_COL_UNROLL2
 #define PLAST_COL_UNROLL2 1
 #endif
+// Leading-axis finalize: lanes per output when there are at least twice as many chunks (1: one
+// lane, batches of 16 loads in sequence). Measured (two alternating runs): 8 lanes took config 1's
+// grad_b (16 chunks) from 9.4-9.9 to 7.3-7.5 us per call and the one-pass epilogue (64 chunks)
+// +3%, the [16384, 4096] bias gradient unchanged; 4 lanes lost 5% on that bias gradient.
+#ifndef PLAST_COL_FIN_Q
+#define PLAST_COL_FIN_Q 8
+#endif
 #ifndef PLAST_COL_BLOCKS
 #define PLAST_COL_BLOCKS 1024  // workgroups a leading-axis reduction is chunked up to
 #endif

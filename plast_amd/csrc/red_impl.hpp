@@ -665,6 +665,50 @@ __global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<Prod::NIN> A
   store_final<Comb>(A.out, tbase + int64_t(j) * A.tkst, p, A.post, A.divisor);
 }
 
+// The same merge with Q lanes per output, for many chunks: lane (q, o) merges the q-th run of
+// consecutive chunks of output o in index order (lanes with the same q read consecutive outputs),
+// then the runs merge pairwise through shuffles with the earlier run always on the left, as in
+// red_rows_finalize. One batch of loads per lane instead of segs / 16 batches in sequence.
+template <class Prod, class Comb, int Q>
+__global__ __launch_bounds__(kBlock) void red_cols_finalize_q(RedArgs<Prod::NIN> A, Prod prod) {
+  using Part = typename Comb::Part;
+  constexpr int NIN = Prod::NIN;
+  constexpr uint32_t OPW = 64 / Q;  // outputs per wave
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t(blockIdx.x) * kBlock + threadIdx.x) >> 6;
+  const uint32_t q = lane / OPW;
+  const uint64_t nout = A.rows * A.inner;
+  const uint64_t oi = wave * OPW + (lane % OPW);
+  const bool valid = oi < nout;
+  const uint32_t run = (A.segs + Q - 1) / Q;
+  const uint32_t active = (A.segs + run - 1) / run;  // runs holding at least one chunk
+  Part p = Comb::empty();
+  if (valid && q < active) {
+    const uint32_t s0 = q * run;
+    const uint32_t n = A.segs - s0 < run ? A.segs - s0 : run;
+    p = merge_in_order<Comb>(static_cast<const Part *>(A.part) + uint64_t(s0) * nout + oi, nout,
+                             n);
+  }
+#pragma unroll
+  for (uint32_t off = 1; off < uint32_t(Q); off <<= 1) {
+    const Part o = shfl_down_part(p, int(off * OPW));
+    if ((q & (2 * off - 1)) == 0 && q + off < active) p = Comb::merge(p, o);
+  }
+  if (q != 0 || !valid) return;
+  const uint32_t o = uint32_t(oi / A.inner);
+  const uint64_t j = oi - uint64_t(o) * A.inner;
+  int64_t base[NIN], tbase;
+  decode_outer(A, o, base, tbase);
+  if constexpr (kSerialSum<Comb>) {
+    if (!finite_sum(p)) {
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) base[k] += int64_t(j) * A.kst[k];
+      p = serial_sum_lane(A, prod, base, A.len);
+    }
+  }
+  store_final<Comb>(A.out, tbase + int64_t(j) * A.tkst, p, A.post, A.divisor);
+}
+
 // ------------------------------------------------------------------------- generic kernel
 
 template <int NIN>
@@ -897,7 +941,11 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
       if (vec) red_cols_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
       else red_cols_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
       if (chunks > 1)  // the finalize reads the partials, and the inputs for a serial refold
-        red_cols_finalize<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(A, prod);
+        if (PLAST_COL_FIN_Q > 1 && chunks >= 2 * PLAST_COL_FIN_Q)
+          red_cols_finalize_q<Prod, Comb, PLAST_COL_FIN_Q>
+              <<<ceil_div(nout * PLAST_COL_FIN_Q, kBlock), kBlock, 0, stream()>>>(A, prod);
+        else
+          red_cols_finalize<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(A, prod);
       return true;
     }
   }
