@@ -2,8 +2,9 @@
 training step (the fused relu(X + b) chain, then grad_b = Σ_rows grad_Y through the split
 leading-axis reduction and its finalize) captured once and replayed several times, with fresh
 inputs uploaded eagerly between replays, each replay checked bit for bit against the same step
-run eagerly; plus a flat compiled chain (2^20 elements) captured and replayed, and the error paths
-(nested capture, a launch inside a capture, ending a capture that is not open)."""
+run eagerly; plus a flat compiled chain (2^20 elements), softmax with its backward and the one-pass
+epilogue captured and replayed, and the error paths (nested capture, a launch inside a capture,
+ending a capture that is not open)."""
 from __future__ import annotations
 
 import ctypes as C
@@ -61,6 +62,54 @@ def test_config1_step_replays_match_eager():
             step()                           # the same step, eagerly, on the same inputs
             assert_bits(y_g, Y.numpy(), f"replay {rep}: relu(X + b)")
             assert_bits(gb_g, gb.numpy(), f"replay {rep}: grad_b")
+    finally:
+        L.plast_hip_graph_destroy(graph)
+
+
+def test_softmax_and_one_pass_epilogue_replay():
+    """Softmax (rows in registers), its backward, and the one-pass relu-gradient modulation +
+    bias-gradient sum (the column kernel, its 16 chunks and the 8-lane finalize) captured as one
+    graph; each replay against the same calls run eagerly, bit for bit."""
+    from plast_amd.abi import KernelParams
+    rt = _rt()
+    L = rt.lib()
+    print("graph: softmax + one-pass epilogue", flush=True)
+    R, Cn = 1024, 1000
+    x = rt.DeviceTensor((R, Cn), requires_grad=True, zero=False)
+    y = rt.DeviceTensor((R, Cn), requires_grad=True, zero=False)
+    dout, z, dc = (rt.DeviceTensor((R, Cn), zero=False) for _ in range(3))
+    db = rt.DeviceTensor((Cn,), zero=False)
+    p = KernelParams(1, 0, 0.0)
+
+    def step():
+        rt.forward("softmax", [x], y, p)
+        rt.backward("softmax", [x], y, p)
+        L.relu_grad_modulate_bias_grad_hip(dout.ptr, z.ptr, dc.ptr, db.ptr, R * Cn, Cn, 0.01)
+        L.check("one-pass epilogue")
+
+    rng = np.random.RandomState(2)
+
+    def fresh():
+        for t in (x, y.grad, dout, z):
+            _h2d(t, rng.randn(R, Cn))
+        _h2d(x.grad, np.zeros((R, Cn)))
+
+    fresh()
+    step()                                   # sizes the workspaces outside the capture
+    assert L.plast_hip_capture_begin() == 0
+    step()
+    graph = L.plast_hip_capture_end()
+    L.check("capture")
+    assert graph
+    try:
+        for rep in range(4):
+            fresh()
+            assert L.plast_hip_graph_launch(graph) == 0
+            got = [t.numpy() for t in (y, x.grad, dc, db)]
+            _h2d(x.grad, np.zeros((R, Cn)))
+            step()                           # the same calls, eagerly, on the same inputs
+            for g, t, what in zip(got, (y, x.grad, dc, db), ("y", "dx", "dc", "dbias")):
+                assert_bits(g, t.numpy(), f"replay {rep}: {what}")
     finally:
         L.plast_hip_graph_destroy(graph)
 
