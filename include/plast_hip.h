@@ -296,29 +296,6 @@ int plast_hip_error_count(void);
 const char *plast_hip_last_error(void);
 void plast_hip_clear_error(void);
 
-/* Fused chains (fused_elementwise_hip_forward) of at least 2^20 elements over a flat space, over
- * rows with a re-read bias row or per-row scalars, or over whole transposed-operand tiles, run as a
- * kernel compiled for their tape and layout at first use (hiprtc, cached per distinct tape and
- * layout for the process); every other chain, and every chain in mode 0, runs on the tape
- * interpreter. Both compute the same bits. The environment variable PLAST_HIP_CHAIN_JIT=0 selects
- * mode 0 at first use. Returns the previous mode. No counterpart in the reference, whose chains
- * run as one node per op. */
-int plast_hip_set_chain_jit(int mode);
-/* Launches that ran a compiled chain since the library was loaded. */
-u64 plast_hip_chain_jit_launches(void);
-/* Diagnostic: the HIP source the chain compiler writes for `tape` (bit k of `bcast`: input k is
- * one broadcast scalar), copied into buf (capacity cap, always NUL-terminated). Returns the
- * source's length, 0 for a malformed tape. Needs no device. */
-u64 plast_hip_chain_jit_source(const PlastFusedTape *tape, u32 bcast, char *buf, u64 cap);
-/* The same for the rows form (chains over [rows, inner] where an input is re-read for every row,
- * such as a bias row, or is one scalar per row): bits 0-3 of `pattern` mark per-row scalars, bits
- * 8-11 re-read rows. */
-u64 plast_hip_chain_jit_rows_source(const PlastFusedTape *tape, u32 pattern, char *buf, u64 cap);
-/* The same for the transposed-operand tile form: operand k's role is bits 2k..2k+1 of `roles`
- * (0 staged through LDS, 1 broadcast along the output's inner axis, 2 broadcast along the staged
- * operands' unit axis, 3 read directly). */
-u64 plast_hip_chain_jit_tile_source(const PlastFusedTape *tape, u32 roles, char *buf, u64 cap);
-
 /* Device time between two marks recorded on the library stream, in milliseconds. */
 int plast_hip_timer_begin(void);
 float plast_hip_timer_end(void);

@@ -81,9 +81,7 @@ def build_library(jobs: int | None = None, defines: list[str] | None = None,
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = lib.with_suffix(".so.tmp")
-    # hiprtc: the chain compiler (chain_jit.hip)
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          "-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, lib)
     return lib
 

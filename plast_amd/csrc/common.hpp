@@ -50,6 +50,22 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_TAPE_XCD
 #define PLAST_TAPE_XCD 0
 #endif
+// Flat fused chains (every input unit-stride or one broadcast scalar) run the streaming form of the
+// interpreter: SWPC workgroups of SBLOCK lanes per CU, each walking a contiguous range of float4
+// units SUNROLL per lane at a time, with the next step's operands loaded before the current step is
+// interpreted. STREAM 0 sends them to the one-shot vector kernel instead.
+#ifndef PLAST_TAPE_STREAM
+#define PLAST_TAPE_STREAM 0
+#endif
+#ifndef PLAST_TAPE_SBLOCK
+#define PLAST_TAPE_SBLOCK 256
+#endif
+#ifndef PLAST_TAPE_SWPC
+#define PLAST_TAPE_SWPC 8
+#endif
+#ifndef PLAST_TAPE_SUNROLL
+#define PLAST_TAPE_SUNROLL 1
+#endif
 #ifndef PLAST_TAPE_TILE_ROWS
 #define PLAST_TAPE_TILE_ROWS 2  // fused chains in the transposed-operand tile: rows per evaluation
 #endif
@@ -182,6 +198,8 @@ __device__ __forceinline__ void store_stream(f4 v, f4 *p) {
 
 void report_error(const char *where, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 hipStream_t stream();
+// Compute units of the library's device.
+int num_cus();
 // Called at the end of every entry point: checks the launch and, in synchronous mode, waits.
 void finish(const char *where);
 bool ensure_init();

@@ -71,28 +71,55 @@ bool covers(const Tensor *t, const uint64_t *shape, int rank) {
   return true;
 }
 
-// Accumulate one operand's gradient: elementwise when it has the output's shape, otherwise a
-// deterministic reduction over its broadcast axes (the reference uses `omp atomic` here:
-// kernel_macros.h:283-299).
+// One past the largest element offset that shape and strides address (0 for an empty shape).
+uint64_t extent(const uint64_t *shape, const uint64_t *strides, uint64_t ndim) {
+  uint64_t hi = 0;
+  for (uint64_t d = 0; d < ndim; ++d) {
+    if (shape[d] == 0) return 0;
+    hi += (shape[d] - 1) * strides[d];
+  }
+  return hi + 1;
+}
+
+// Accumulate one operand's gradient. The reference's broadcast backward addresses the gradient
+// buffer with the operand's *data* strides (kernel_macros.h:314-317 passes a->strides as
+// da_strides; its contiguous path indexes da flat, the same offsets for a contiguous operand). A
+// view's grad keeps the layout it was allocated with (tensor.c:66-78) while the view's forward
+// rewrote its data strides (shape_ops.c:59-80), so on a transposed view the two layouts differ, and
+// this follows the reference. Elementwise when those offsets are distinct, otherwise a
+// deterministic reduction over the axes that repeat an offset (broadcast or expanded axes; the
+// reference uses `omp atomic` here: kernel_macros.h:283-299). Offsets past the gradient's own
+// extent (the reference would write out of bounds) are refused.
 template <class Elem, class Term>
 void grad_into(const Tensor *x, const Tensor *out, const Tensor *a, const Tensor *b,
                const Elem &elem, const Term &term, const char *where) {
   const Tensor *g = out->grad;
+  const int rank = int(g->ndim);
+  int64_t tst[kMaxRank];
+  bcast_strides(x, g->shape, rank, tst);
+  const uint64_t need = extent(x->shape, x->strides, x->ndim);
+  const uint64_t have = extent(x->grad->shape, x->grad->strides, x->grad->ndim);
+  if (need > have) {
+    report_error(where, "the operand's strides address %llu gradient elements, its gradient holds "
+                 "%llu", (unsigned long long)need, (unsigned long long)have);
+    return;
+  }
+  bool repeats = false;
+  for (int d = 0; d < rank; ++d) repeats = repeats || (tst[d] == 0 && g->shape[d] > 1);
   Space s;
-  init_space(s, g->shape, int(g->ndim));
-  if (covers(x, g->shape, int(g->ndim))) {
-    set_operand(s, 0, x->grad);
+  init_space(s, g->shape, rank);
+  if (!repeats) {
+    for (int d = 0; d < rank; ++d) s.st[0][d] = s.st[4][d] = tst[d];
     set_own(s, 1, g);
     set_operand(s, 2, a);
     set_operand(s, 3, b);
-    set_operand(s, 4, x->grad);
     const void *ins[4] = {x->grad->data, g->data, a->data, b->data};
     launch_elementwise(elem, ins, x->grad->data, s, where);
   } else {
     set_own(s, 0, g);
     set_operand(s, 1, a);
     set_operand(s, 2, b);
-    set_operand(s, 3, x->grad);
+    for (int d = 0; d < rank; ++d) s.st[3][d] = tst[d];
     const void *ins[3] = {g->data, a->data, b->data};
     reduce_accumulate(term, ins, static_cast<float *>(x->grad->data), s, where);
   }
@@ -242,6 +269,18 @@ void expand_like_forward(const Tensor **in, Tensor *out) {
       const uint64_t s = d - lead;
       out->strides[d] = (a->shape[s] == 1 && out->shape[d] > 1) ? 0 : a->strides[s];
     }
+  }
+}
+
+// A fused chain on the interpreter instantiated for op set OPS and its input count.
+template <uint32_t OPS>
+void launch_tape(const PlastFusedTape &t, uint64_t se, uint32_t neg_simd, int nin,
+                 const void *const *ins, void *out, const Space &s, const char *where) {
+  switch (nin) {
+  case 1: launch_elementwise(TapeBody<1, OPS>{t, se, neg_simd}, ins, out, s, where); break;
+  case 2: launch_elementwise(TapeBody<2, OPS>{t, se, neg_simd}, ins, out, s, where); break;
+  case 3: launch_elementwise(TapeBody<3, OPS>{t, se, neg_simd}, ins, out, s, where); break;
+  default: launch_elementwise(TapeBody<4, OPS>{t, se, neg_simd}, ins, out, s, where); break;
   }
 }
 
@@ -421,28 +460,28 @@ void fused_elementwise_hip_forward(const Tensor **inputs, Tensor *output, Kernel
   }
   const int nin = int(tape->num_inputs);
   set_own(s, nin, output);
-  // Every intermediate of the unfused chain is a fresh contiguous tensor, so the reference's neg
-  // takes its contiguous path whenever the chain's output is contiguous.
-  const uint64_t se = contiguous(output) ? simd_end(n) : 0;
+  // The reference's neg takes its 8-wide SIMD path (0 - x below simd_end) only when its input and
+  // its output are both contiguous (DEFINE_UNARY_CPU_FORWARD, kernel_macros.h:19-31), and -x
+  // otherwise. Every intermediate of the unfused chain is a fresh contiguous tensor, so only a NEG
+  // reading the loaded input directly or writing the chain's output can meet a strided tensor.
+  uint32_t neg_simd = 0;
+  for (uint32_t i = 1; i < tape->num_ins; ++i) {
+    if (tape->ins[i].op != TAPE_NEG) continue;
+    const bool in_ok = i > 1 || contiguous(inputs[tape->ins[0].idx]);
+    const bool out_ok = i + 1 < tape->num_ins || contiguous(output);
+    if (in_ok && out_ok) neg_simd |= 1u << i;
+  }
+  const uint64_t se = simd_end(n);
   (void)all_contig;
-  bool trig = false;
-  for (uint32_t i = 0; i < tape->num_ins; ++i)
-    trig = trig || tape->ins[i].op == TAPE_SIN || tape->ins[i].op == TAPE_COS ||
-           tape->ins[i].op == TAPE_TAN;
-  if (trig) {
-    switch (nin) {
-    case 1: { TapeBody<1, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    case 2: { TapeBody<2, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    case 3: { TapeBody<3, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    default: { TapeBody<4, true> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    }
-  } else {
-    switch (nin) {
-    case 1: { TapeBody<1, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    case 2: { TapeBody<2, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    case 3: { TapeBody<3, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    default: { TapeBody<4, false> b{*tape, se}; launch_elementwise(b, ins, output->data, s, where); break; }
-    }
+  switch (tape_ops_class(*tape)) {
+  case kTapeArith: launch_tape<kTapeArith>(*tape, se, neg_simd, nin, ins, output->data, s, where); break;
+  case kTapeExp: launch_tape<kTapeExp>(*tape, se, neg_simd, nin, ins, output->data, s, where); break;
+  case kTapeExp | kTapeLog:
+    launch_tape<kTapeExp | kTapeLog>(*tape, se, neg_simd, nin, ins, output->data, s, where);
+    break;
+  default:
+    launch_tape<kTapeExp | kTapeLog | kTapeTrig>(*tape, se, neg_simd, nin, ins, output->data, s, where);
+    break;
   }
   finish(where);
 }

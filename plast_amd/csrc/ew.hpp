@@ -88,6 +88,14 @@ struct ScalarBody {
     for (int u = 0; u < U; ++u)
       if (valid[u]) acc[u] = eval4(x[u], idx[u]);
   }
+  // the kernels' common interface with the tape body, which reads per-wave state first
+  __device__ __forceinline__ uint32_t load_words() const { return 0; }
+  template <int U, int N>
+  __device__ __forceinline__ void eval_units_with(uint32_t, const f4 (&x)[U][N],
+                                                  const uint64_t (&idx)[U], const bool (&valid)[U],
+                                                  f4 (&acc)[U]) const {
+    eval_units<U, N>(x, idx, valid, acc);
+  }
   __device__ __forceinline__ f4 eval4(const f4 *x, uint64_t idx) const {
     const Derived &d = static_cast<const Derived &>(*this);
     constexpr int N = Derived::NIN;
@@ -176,20 +184,45 @@ struct AccumDivBody : ScalarBody<AccumDivBody> {
   }
 };
 
-// Runtime tape interpreter for fused chains. Every field read is a scalar load of the kernel
-// argument and every branch is on an SGPR value, so the interpretation costs scalar instructions
-// only. The tape loop is the outer loop, so each dispatch is paid once per U float4 units.
-// TRIG: whether sin/cos/tan are compiled in. Their argument reduction needs many registers, so
-// tapes without them run an instantiation that leaves those cases out (and keeps more waves
-// resident).
-template <int N, bool TRIG>
+// Op classes a fused chain's kernel is compiled for (a bit set: the OPS parameter of TapeBody).
+// The arithmetic ops (add, sub, mul, div, leaky relu, neg, abs) are always in; each class below
+// adds the ocml routine it needs. A tape runs on the smallest instantiated set that holds its ops
+// (tape_ops_class), so a chain without exp or log carries none of their code or registers.
+enum TapeOps : uint32_t { kTapeArith = 0, kTapeExp = 1, kTapeLog = 2, kTapeTrig = 4 };
+
+// The instantiated sets: arithmetic only, + exp, + exp and log, everything.
+inline uint32_t tape_ops_class(const PlastFusedTape &t) {
+  uint32_t m = 0;
+  for (uint32_t i = 0; i < t.num_ins; ++i) {
+    const uint8_t op = t.ins[i].op;
+    if (op == TAPE_EXP) m |= kTapeExp;
+    else if (op == TAPE_LOG) m |= kTapeLog;
+    else if (op == TAPE_SIN || op == TAPE_COS || op == TAPE_TAN) m |= kTapeTrig;
+  }
+  if (m & kTapeTrig) return kTapeExp | kTapeLog | kTapeTrig;
+  if (m & kTapeLog) return kTapeExp | kTapeLog;
+  return m;
+}
+
+// Tape interpreter for fused chains. Every field read is a scalar load of the kernel argument and
+// every branch is on an SGPR value, so the interpretation costs scalar instructions only. The tape
+// loop is the outer loop, so each dispatch is paid once per U float4 units. OPS (TapeOps bits):
+// the op classes compiled in; a tape must hold no op outside them (the host picks OPS with
+// tape_ops_class).
+template <int N, uint32_t OPS>
 struct TapeBody {
   static constexpr int NIN = N;
   static constexpr bool kTape = true;
   static constexpr bool kTileFixed3 = true;
   static constexpr int kTileRows = PLAST_TAPE_TILE_ROWS;
+  static constexpr bool kExp = (OPS & kTapeExp) != 0;
+  static constexpr bool kLog = (OPS & kTapeLog) != 0;
+  static constexpr bool kTrig = (OPS & kTapeTrig) != 0;
   PlastFusedTape t;
   uint64_t simd_end;
+  // bit i: the NEG at instruction i follows the reference's contiguous path (0 - x below simd_end,
+  // -x in the tail); a NEG whose bit is clear takes its strided path (-x everywhere)
+  uint32_t neg_simd;
 
   template <class F>
   __device__ __forceinline__ static f4 map(f4 a, F f) {
@@ -202,14 +235,26 @@ struct TapeBody {
   template <int U>
   __device__ __forceinline__ void eval_units(const f4 (&x)[U][N], const uint64_t (&idx)[U],
                                              const bool (&valid)[U], f4 (&acc)[U]) const {
-    (void)valid;
-    // The tape's 2 * PLAST_TAPE_MAX_INS dwords, one per lane (lane 2i: op/src/idx/acc_rhs bytes of
-    // instruction i; lane 2i+1: its immediate), read back with v_readlane. A scalar load per
-    // instruction would need a wait on the shared scalar/LDS counter, which also drains a tile
-    // kernel's outstanding LDS reads.
+    eval_units_with<U>(load_words(), x, idx, valid, acc);
+  }
+
+  // The tape's 2 * PLAST_TAPE_MAX_INS dwords, one per lane (lane 2i: op/src/idx/acc_rhs bytes of
+  // instruction i; lane 2i+1: its immediate), read back with v_readlane. A scalar load per
+  // instruction would need a wait on the shared scalar/LDS counter, which also drains a tile
+  // kernel's outstanding LDS reads. Every lane of the wave must execute this load (v_readlane
+  // reads lanes the caller's branch may have switched off), and a kernel that prefetches operands
+  // loads the words once up front: waiting for a load issued after a prefetch waits for the
+  // prefetch too.
+  __device__ __forceinline__ uint32_t load_words() const {
     static_assert(sizeof(PlastTapeIns) == 8, "tape instruction is two dwords");
-    const uint32_t words =
-        reinterpret_cast<const uint32_t *>(t.ins)[__lane_id() & (2 * PLAST_TAPE_MAX_INS - 1)];
+    return reinterpret_cast<const uint32_t *>(t.ins)[__lane_id() & (2 * PLAST_TAPE_MAX_INS - 1)];
+  }
+
+  template <int U>
+  __device__ __forceinline__ void eval_units_with(uint32_t words, const f4 (&x)[U][N],
+                                                  const uint64_t (&idx)[U], const bool (&valid)[U],
+                                                  f4 (&acc)[U]) const {
+    (void)valid;
     const uint32_t w0x = uint32_t(__builtin_amdgcn_readlane(int(words), 0));
     select_input(x, int((w0x >> 16) & 0xffu), acc);
     // not unrolled: the loop sits outside any lane-divergent branch, so i stays uniform
@@ -262,36 +307,43 @@ struct TapeBody {
           acc[u] = map(acc[u], [imm](float v) { return v > 0.0f ? v : v * imm; });
         break;
       case TAPE_EXP:
+        if constexpr (kExp) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return expf(v); });
+          for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return expf(v); });
+        }
         break;
       case TAPE_LOG:
+        if constexpr (kLog) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return logf(v); });
+          for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return logf(v); });
+        }
         break;
-      case TAPE_NEG:
+      case TAPE_NEG: {
+        const bool contig = (neg_simd >> i & 1u) != 0u;
 #pragma unroll
         for (int u = 0; u < U; ++u)
-          acc[u] = idx[u] < simd_end ? f4(0.0f) - acc[u] : map(acc[u], [](float v) { return -v; });
+          acc[u] = contig && idx[u] < simd_end ? f4(0.0f) - acc[u]
+                                               : map(acc[u], [](float v) { return -v; });
         break;
+      }
       case TAPE_ABS:
 #pragma unroll
         for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return fabsf(v); });
         break;
       case TAPE_SIN:
-        if constexpr (TRIG) {
+        if constexpr (kTrig) {
 #pragma unroll
           for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return sinf(v); });
         }
         break;
       case TAPE_COS:
-        if constexpr (TRIG) {
+        if constexpr (kTrig) {
 #pragma unroll
           for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return cosf(v); });
         }
         break;
       case TAPE_TAN:
-        if constexpr (TRIG) {
+        if constexpr (kTrig) {
 #pragma unroll
           for (int u = 0; u < U; ++u) acc[u] = map(acc[u], [](float v) { return tanf(v); });
         }
@@ -330,7 +382,7 @@ struct TapeBody {
 #pragma unroll
     for (int k = 0; k < N; ++k) x[0][k] = f4(v[k]);
     // a lone element decides the NEG rule for itself
-    TapeBody<N, TRIG> me = *this;
+    TapeBody<N, OPS> me = *this;
     me.simd_end = idx < simd_end ? ~uint64_t(0) : 0;
     const uint64_t i0[1] = {0};
     const bool ok[1] = {true};

@@ -5,7 +5,6 @@
 #include <type_traits>
 #include <utility>
 
-#include "chain_jit.hpp"
 #include "ew.hpp"
 
 namespace plast {
@@ -66,6 +65,7 @@ __global__ __launch_bounds__((VecLaunch<Body, REUSE>::block)) void ew_vec_kernel
   constexpr bool kNtStore = PLAST_EW_NT_STORE < 0 ? REUSE : PLAST_EW_NT_STORE != 0;
   const uint32_t bid = VecLaunch<Body, REUSE>::xcd ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint64_t base = uint64_t(bid) * (kEwBlock * kEwUnroll) + threadIdx.x;
+  const uint32_t words = body.load_words();
   f4 x[kEwUnroll][NIN];
   int64_t oo[kEwUnroll];
 #pragma unroll
@@ -111,22 +111,101 @@ __global__ __launch_bounds__((VecLaunch<Body, REUSE>::block)) void ew_vec_kernel
     valid[u] = base + uint64_t(u) * kEwBlock < A.units;
   }
   f4 r[kEwUnroll];
-  body.template eval_units<kEwUnroll>(x, idx, valid, r);
+  body.template eval_units_with<kEwUnroll>(words, x, idx, valid, r);
 #pragma unroll
   for (int u = 0; u < kEwUnroll; ++u)
     if (valid[u]) store_stream<kNtStore>(r[u], reinterpret_cast<f4 *>(A.out + oo[u]));
 }
 
+// Streaming form of a flat fused chain (Body a TapeBody): every input is unit-stride or one
+// broadcast scalar (bit k of A.bcast_inner). The grid is a fixed number of workgroups; workgroup b
+// (XCD-contiguous numbering) walks units [b * per_block, (b + 1) * per_block) in steps of
+// SUNROLL * SBLOCK units, and loads the next step's operands before interpreting the current one,
+// so the interpreter's scalar dispatch overlaps the memory latency instead of adding to it. Each
+// wave reads and writes whole 1 KiB runs per operand per unit. per_block is a multiple of the step.
+template <class Body>
+__global__ __launch_bounds__(PLAST_TAPE_SBLOCK) void ew_tape_stream_kernel(EwArgs<Body::NIN> A,
+                                                                           Body body,
+                                                                           uint64_t per_block) {
+  constexpr int NIN = Body::NIN;
+  constexpr int B = PLAST_TAPE_SBLOCK, U = PLAST_TAPE_SUNROLL;
+  const uint64_t beg = uint64_t(xcd_block(blockIdx.x, gridDim.x)) * per_block;
+  if (beg >= A.units) return;
+  const uint64_t end = beg + per_block < A.units ? beg + per_block : A.units;
+  // broadcast scalars: loaded once
+  f4 bc[NIN];
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) bc[k] = (A.bcast_inner >> k & 1u) ? f4(A.in[k][0]) : f4(0.0f);
+  auto load = [&](uint64_t b0, f4 (&x)[U][NIN]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t q = b0 + uint64_t(u) * B + threadIdx.x;
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) {
+        if (A.bcast_inner >> k & 1u) x[u][k] = bc[k];
+        else if (q < end) x[u][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A.in[k]) + q);
+      }
+    }
+  };
+  const uint32_t words = body.load_words();
+  // one step: interpret the units of step b0 held in x, store them
+  auto step = [&](uint64_t b0, const f4 (&x)[U][NIN]) {
+    uint64_t idx[U];
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t q = b0 + uint64_t(u) * B + threadIdx.x;
+      idx[u] = q * 4;
+      valid[u] = q < end;
+    }
+    f4 r[U];
+    body.template eval_units_with<U>(words, x, idx, valid, r);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (valid[u]) reinterpret_cast<f4 *>(A.out)[idx[u] / 4] = r[u];
+  };
+  // Two register sets used in turn, so a step's operands are never copied: a copy out of a
+  // set whose loads are still in flight would wait for them and serialise memory and interpretation.
+  constexpr uint64_t S = uint64_t(B) * U;
+  f4 xa[U][NIN], xb[U][NIN];
+  load(beg, xa);
+  for (uint64_t b0 = beg; b0 < end; b0 += 2 * S) {
+    if (b0 + S < end) load(b0 + S, xb);
+    step(b0, xa);
+    if (b0 + S >= end) break;
+    if (b0 + 2 * S < end) load(b0 + 2 * S, xa);
+    step(b0 + S, xb);
+  }
+}
+
+// Launch the streaming form over A.units float4 units (flat space, A filled by the vector path).
+template <class Body>
+void launch_tape_stream(const EwArgs<Body::NIN> &A, const Body &body) {
+  constexpr uint64_t step = uint64_t(PLAST_TAPE_SBLOCK) * PLAST_TAPE_SUNROLL;
+  const uint64_t steps = (A.units + step - 1) / step;
+  uint64_t grid = uint64_t(num_cus()) * PLAST_TAPE_SWPC;
+  if (grid > steps) grid = steps;
+  const uint64_t per_block = (steps + grid - 1) / grid * step;
+  grid = (A.units + per_block - 1) / per_block;
+  ew_tape_stream_kernel<Body><<<unsigned(grid), PLAST_TAPE_SBLOCK, 0, stream()>>>(A, body, per_block);
+}
+
 // Generic kernel: any strides, one element per lane per step. IDX64 selects 64-bit division for
-// spaces of 2^32 elements or more.
+// spaces of 2^32 elements or more. The loop runs per workgroup, not per lane, so every lane is
+// active when the body is evaluated (the tape interpreter reads its instruction words across the
+// wave's lanes); lanes past the end only skip their loads and their store.
 template <class Body, bool IDX64>
 __global__ __launch_bounds__(kBlock) void ew_generic_kernel(EwArgs<Body::NIN> A, Body body) {
   constexpr int NIN = Body::NIN;
   const uint64_t stride = uint64_t(gridDim.x) * kBlock;
-  for (uint64_t e = uint64_t(blockIdx.x) * kBlock + threadIdx.x; e < A.n; e += stride) {
+  for (uint64_t e0 = uint64_t(blockIdx.x) * kBlock; e0 < A.n; e0 += stride) {
+    const uint64_t e = e0 + threadIdx.x;
+    const bool in_range = e < A.n;
     int64_t off[NIN] = {};
     int64_t ooff = 0;
-    if constexpr (IDX64) {
+    if (!in_range) {
+      // nothing to address: the loads and the store below are skipped
+    } else if constexpr (IDX64) {
       uint64_t rem = e;
       for (int d = A.rank - 1; d >= 0; --d) {
         const uint64_t ext = A.shape64[d];
@@ -149,8 +228,9 @@ __global__ __launch_bounds__(kBlock) void ew_generic_kernel(EwArgs<Body::NIN> A,
     }
     float v[NIN];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) v[k] = A.in[k][off[k]];
-    A.out[ooff] = body.eval(v, e);
+    for (int k = 0; k < NIN; ++k) v[k] = in_range ? A.in[k][off[k]] : 0.0f;
+    const float r = body.eval(v, e);
+    if (in_range) A.out[ooff] = r;
   }
 }
 
@@ -199,6 +279,7 @@ __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, 
   }
   const uint32_t q0 = tqi * kTile, p0 = tpi * kTile;
   const int t = threadIdx.x;
+  const uint32_t words = body.load_words();
   // stage: thread t loads float4 (along q) of rows b = t/16 + 16r of the tile
 #pragma unroll
   for (int k = 0; k < NIN; ++k) {
@@ -283,7 +364,7 @@ __global__ __launch_bounds__(kBlock) void ew_tile_kernel(TileArgs<Body::NIN> A, 
       }
     }
     f4 res[1];
-    body.template eval_units<1>(x, idx, valid, res);
+    body.template eval_units_with<1>(words, x, idx, valid, res);
     if (valid[0])
       store_stream<PLAST_TILE_NT_STORE>(res[0], reinterpret_cast<f4 *>(A.out + base[NIN] +
                                                    int64_t(q0 + a) * A.qst[NIN] + int64_t(p0 + b4)));
@@ -330,6 +411,7 @@ __global__ __launch_bounds__(kBlock) void ew_tile_fixed_kernel(TileArgs<Body::NI
   const int64_t q0 = int64_t(tqi) * kTile, p0 = int64_t(tpi) * kTile;
   const int t = threadIdx.x;
   const uint32_t l4 = (t & 15) * 4, r16 = t >> 4;
+  const uint32_t words = body.load_words();
 
   // staged (role 0): float4 along q of tile rows p0 + r16 + 16r; role 1: the scalar of each output
   // row q0 + r16 + 16r; role 2: one float4 along p; role 3: float4 along p of each output row
@@ -406,7 +488,7 @@ __global__ __launch_bounds__(kBlock) void ew_tile_fixed_kernel(TileArgs<Body::NI
       valid[u] = true;
     }
     f4 res[TR];
-    body.template eval_units<TR>(x, idx, valid, res);
+    body.template eval_units_with<TR>(words, x, idx, valid, res);
 #pragma unroll
     for (int u = 0; u < TR; ++u)
       store_stream<PLAST_TILE_NT_STORE>(res[u], reinterpret_cast<f4 *>(dst + (h * TR + u) * dstep));
@@ -538,34 +620,6 @@ bool try_tile(const Body &body, const void *const *in, void *out, const Space &s
   A.dtq = MagicDiv::make(A.tq);
   A.dtp = MagicDiv::make(A.tp);
   const bool full = A.eq % kTile == 0 && A.ep % kTile == 0;
-  if constexpr (Body::kTape) {
-    // whole tiles: the tape's compiled tile form, when the chain compiler takes it
-    if (full) {
-      ChainTileGeometry g;
-      memset(&g, 0, sizeof g);
-      for (int k = 0; k <= NIN; ++k) {
-        const int gk = k < NIN ? k : PLAST_TAPE_MAX_INPUTS;
-        if (k < NIN) g.in[k] = A.in[k];
-        for (int d = 0; d < nb; ++d) g.bst[gk][d] = A.bst[k][d];
-        g.qst[gk] = A.qst[k];
-        g.pst[gk] = A.pst[k];
-      }
-      g.out = A.out;
-      for (int d = 0; d < nb; ++d) {
-        g.bdv[d][0] = A.bdv[d].mul;
-        g.bdv[d][1] = A.bdv[d].shift;
-        g.bdv[d][2] = A.bdv[d].d;
-      }
-      g.nbatch = uint32_t(nb);
-      g.tq = A.tq;
-      g.tp = A.tp;
-      g.dtq[0] = A.dtq.mul, g.dtq[1] = A.dtq.shift, g.dtq[2] = A.dtq.d;
-      g.dtp[0] = A.dtp.mul, g.dtp[1] = A.dtp.shift, g.dtp[2] = A.dtp.d;
-      if (chain_jit_tile_launch(body.t, g, roles, s.numel(), body.simd_end, unsigned(blocks),
-                                lds_bytes))
-        return true;
-    }
-  }
   if (full && launch_tile_fixed(A, body, roles, unsigned(blocks), lds_bytes)) return true;
   if (direct) ew_tile_kernel<Body, true><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
   else ew_tile_kernel<Body, false><<<unsigned(blocks), kBlock, lds_bytes, stream()>>>(A, body);
@@ -631,18 +685,9 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
     if constexpr (Body::kTape) {
-      // a flat chain over streamed inputs and broadcast scalars: its compiled form, one float4 per
-      // lane (false when the chain compiler does not take it; the interpreter below then runs)
-      if (in_ax == 0 && (A.reused & ~A.bcast_inner) == 0 &&
-          chain_jit_launch(body.t, A.in, A.bcast_inner, A.out, A.units, body.simd_end))
+      if (PLAST_TAPE_STREAM && in_ax == 0 && (A.reused & ~A.bcast_inner) == 0) {
+        launch_tape_stream(A, body);
         return true;
-      // rows with a re-read bias row or per-row scalars: the rows form
-      if (in_ax == 1) {
-        int64_t ist[PLAST_TAPE_MAX_INPUTS] = {};
-        for (int k = 0; k < NIN; ++k) ist[k] = A.ist[k][0];
-        if (chain_jit_rows_launch(body.t, A.in, ist, A.bcast_inner, A.reused & ~A.bcast_inner,
-                                  A.out, A.ost[0], A.units, uint32_t(inner / 4), body.simd_end))
-          return true;
       }
     }
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy

@@ -940,7 +940,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
       const dim3 grid{unsigned(base_blocks), unsigned(chunks), 1u};
       if (vec) red_cols_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
       else red_cols_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
-      if (chunks > 1)  // the finalize reads the partials, and the inputs for a serial refold
+      if (chunks > 1) {  // the finalize reads the partials, and the inputs for a serial refold
         // chunks > 1 only when base_blocks < PLAST_COL_BLOCKS, so nout * Q lanes (at most
         // PLAST_COL_BLOCKS * 256 * Q) stay far inside one launch
         if (PLAST_COL_FIN_Q > 1 && chunks >= 2 * PLAST_COL_FIN_Q)
@@ -948,6 +948,7 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
               <<<ceil_div(nout * PLAST_COL_FIN_Q, kBlock), kBlock, 0, stream()>>>(A, prod);
         else
           red_cols_finalize<Prod, Comb><<<ceil_div(nout, kBlock), kBlock, 0, stream()>>>(A, prod);
+      }
       return true;
     }
   }

@@ -19,6 +19,7 @@ constexpr int kSlots = 3;
 void *g_ws[kSlots] = {};
 size_t g_ws_bytes[kSlots] = {};
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
+int g_cus = 256;  // compute units of the device (MI355X: 256), read at init
 }  // namespace
 
 void report_error(const char *where, const char *fmt, ...) {
@@ -38,6 +39,7 @@ bool ensure_init() {
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&g_t0);
   if (e == hipSuccess) e = hipEventCreate(&g_t1);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, g_device);
   if (e != hipSuccess) {
     report_error("init", "device %d: %s", g_device, hipGetErrorString(e));
     return false;
@@ -50,6 +52,8 @@ hipStream_t stream() {
   ensure_init();
   return g_stream;
 }
+
+int num_cus() { return g_cus > 0 ? g_cus : 1; }
 
 void finish(const char *where) {
   hipError_t e = hipGetLastError();

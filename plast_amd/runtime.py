@@ -47,11 +47,6 @@ class Library:
         sig = {
             "plast_hip_init": ([C.c_int], C.c_int),
             "plast_hip_set_sync": ([C.c_int], None),
-            "plast_hip_set_chain_jit": ([C.c_int], C.c_int),
-            "plast_hip_chain_jit_launches": ([], C.c_uint64),
-            "plast_hip_chain_jit_source": ([C.c_void_p, C.c_uint32, C.c_char_p, C.c_uint64], C.c_uint64),
-            "plast_hip_chain_jit_tile_source": ([C.c_void_p, C.c_uint32, C.c_char_p, C.c_uint64], C.c_uint64),
-            "plast_hip_chain_jit_rows_source": ([C.c_void_p, C.c_uint32, C.c_char_p, C.c_uint64], C.c_uint64),
             "plast_hip_synchronize": ([], C.c_int),
             "plast_hip_capture_begin": ([], C.c_int),
             "plast_hip_capture_end": ([], C.c_void_p),

@@ -21,6 +21,10 @@ class Arr:
     seed: int = 0
     transpose: tuple | None = None   # (d0, d1): present a transposed view of a base of `shape`
     requires_grad: bool = False
+    # a transposed view's gradient: False, an alias of the base's gradient with the view's strides;
+    # True, a buffer of its own, contiguous in the view's shape, which is how the reference
+    # allocates every op output, views included (plast/tensor.py:114-128, src/core/tensor.c:66-78)
+    own_grad: bool = False
 
     def base_array(self) -> np.ndarray:
         rng = np.random.RandomState(self.seed)
@@ -70,6 +74,11 @@ class Case:
     exact: bool = True           # bit-exact expected between oracle and reference
     dout_seed: int = 99
     tags: set = field(default_factory=set)
+    # seed of the values each input gradient holds before the backward (None: zeros), so the
+    # accumulation da += ... is compared past its first term
+    grad_init: int | None = None
+    # the op's two inputs are one tensor (x * x): both gradients accumulate into one buffer
+    same_input: bool = False
 
     def kparams(self) -> KernelParams:
         d, k, f = self.params
@@ -207,6 +216,73 @@ def build_cases() -> list[Case]:
         out[ax[0]], out[ax[1]] = out[ax[1]], out[ax[0]]
         cases.append(Case(f"transpose_bwd_{sh}_{ax}", "transpose", "bwd",
                           [Arr(sh, "normal", s(), requires_grad=True)], tuple(out), (ax[0], ax[1], 0.0)))
+        cases.append(Case(f"transpose_bwd_{sh}_{ax}_acc", "transpose", "bwd",
+                          [Arr(sh, "normal", s(), requires_grad=True)], tuple(out), (ax[0], ax[1], 0.0),
+                          grad_init=s()))
+
+    # ---- binary backward on a transposed view with the reference's own-gradient layout: the
+    # gradient buffer is contiguous in the view's shape, and the reference addresses it with the
+    # view's data strides (kernel_macros.h:314-317)
+    for op in BINARY:
+        dist_b = "pos" if op == "div" else "normal"
+        cases.append(Case(f"{op}_bwd_owngrad_transposed_bcast", op, "bwd",
+                          [Arr((3, 6, 5), "normal", s(), transpose=(1, 2), requires_grad=True,
+                               own_grad=True), Arr((5, 1), dist_b, s())], (3, 5, 6)))
+        cases.append(Case(f"{op}_bwd_owngrad_both_transposed", op, "bwd",
+                          [Arr((4, 7), "normal", s(), transpose=(0, 1), requires_grad=True,
+                               own_grad=True),
+                           Arr((4, 7), dist_b, s(), transpose=(0, 1), requires_grad=True,
+                               own_grad=True)], (7, 4)))
+        cases.append(Case(f"{op}_bwd_owngrad_transposed_bcast_both", op, "bwd",
+                          [Arr((3, 6, 5), "normal", s(), transpose=(1, 2), requires_grad=True,
+                               own_grad=True),
+                           Arr((5, 1), dist_b, s(), requires_grad=True)], (3, 5, 6), exact=False))
+    for op in UNARY[:3] + ["leaky_relu"]:
+        dist = "pos" if op == "log" else "normal"
+        cases.append(Case(f"{op}_bwd_owngrad_transposed", op, "bwd",
+                          [Arr((4, 7), dist, s(), transpose=(0, 1), requires_grad=True,
+                               own_grad=True)], (7, 4), (0, 0, 0.01)))
+    for op in REDUCE:
+        for dim in (0, 1, DIM_ALL):
+            cases.append(Case(f"{op}_bwd_owngrad_transposed_d{dim}", op, "bwd",
+                              [Arr((5, 6), "normal", s(), transpose=(0, 1), requires_grad=True,
+                                   own_grad=True)], _red_shape((6, 5), dim, 0), (dim, 0, 0.0)))
+
+    # ---- backward into gradients that already hold values (a second step without zero_grad, or
+    # a tensor used twice): the reference accumulates (da += ...), so every term is compared
+    for op in BINARY:
+        dist_b = "pos" if op == "div" else "normal"
+        for sh in [(37,), (3, 2, 4)]:
+            cases.append(Case(f"{op}_bwd_acc_{sh}", op, "bwd",
+                              [Arr(sh, "normal", s(), requires_grad=True),
+                               Arr(sh, dist_b, s(), requires_grad=True)], sh, grad_init=s()))
+        cases.append(Case(f"{op}_bwd_acc_transposed", op, "bwd",
+                          [Arr((4, 7), "normal", s(), transpose=(0, 1), requires_grad=True),
+                           Arr((7, 4), dist_b, s(), requires_grad=True)], (7, 4), grad_init=s()))
+        cases.append(Case(f"{op}_bwd_acc_bc", op, "bwd",
+                          [Arr((2, 3, 4), "normal", s(), requires_grad=True),
+                           Arr((3, 1), dist_b, s(), requires_grad=True)], (2, 3, 4),
+                          exact=False, grad_init=s()))
+        # x op x: one tensor as both inputs, so both gradients land in one buffer, A's first
+        for sh in [(37,), (3, 2, 4)]:
+            cases.append(Case(f"{op}_bwd_same_input_{sh}", op, "bwd",
+                              [Arr(sh, dist_b, s(), requires_grad=True)] * 2, sh,
+                              grad_init=s(), same_input=True))
+        cases.append(Case(f"{op}_bwd_same_input_transposed", op, "bwd",
+                          [Arr((4, 7), dist_b, s(), transpose=(0, 1), requires_grad=True)] * 2,
+                          (7, 4), grad_init=s(), same_input=True))
+    for op in UNARY:
+        dist = "pos" if op == "log" else "normal"
+        for sh, tr in [((37,), None), ((3, 2, 4), None), ((4, 7), (0, 1))]:
+            cases.append(Case(f"{op}_bwd_acc_{sh}{'_T' if tr else ''}", op, "bwd",
+                              [Arr(sh, dist, s(), transpose=tr, requires_grad=True)],
+                              (sh[1], sh[0]) if tr else sh, (0, 0, 0.01), grad_init=s()))
+    for op in REDUCE:
+        for dim in (0, 1, DIM_ALL):
+            cases.append(Case(f"{op}_bwd_acc_d{dim}", op, "bwd",
+                              [Arr((6, 9), "ties" if op in ("max", "min") else "normal", s(),
+                                   requires_grad=True)],
+                              _red_shape((6, 9), dim, 0), (dim, 0, 0.0), grad_init=s()))
     return cases
 
 
@@ -220,7 +296,7 @@ class Backend:
     def tensor(self, arr: np.ndarray, requires_grad: bool):
         raise NotImplementedError
 
-    def view(self, base, shape, strides):
+    def view(self, base, shape, strides, own_grad=False):
         raise NotImplementedError
 
     def empty(self, shape, dtype: str, requires_grad: bool = False):
@@ -238,6 +314,10 @@ class Backend:
     def read_grad(self, t) -> np.ndarray:
         raise NotImplementedError
 
+    def grad_size(self, t) -> int:
+        """Elements of the buffer t's gradient lives in (set_grad writes that many, in order)."""
+        raise NotImplementedError
+
     def set_grad(self, t, arr: np.ndarray):
         raise NotImplementedError
 
@@ -250,13 +330,21 @@ def materialize(be: Backend, a: Arr):
     d0, d1 = a.transpose
     st = list(np.array(base_arr.strides) // base_arr.itemsize)
     st[d0], st[d1] = st[d1], st[d0]
-    v = be.view(base, a.view_shape, st)
+    v = be.view(base, a.view_shape, st, own_grad=a.own_grad)
     return v, base_arr
+
+
+def grad_init_values(c: Case, k: int, size: int) -> np.ndarray:
+    """The values input k's gradient buffer holds before the backward, in buffer order."""
+    return np.random.RandomState(c.grad_init + 7 * k).randn(size).astype(np.float32)
 
 
 def run_case(be: Backend, c: Case) -> dict:
     res = {}
-    ins = [materialize(be, a)[0] for a in c.inputs]
+    if c.same_input:
+        ins = [materialize(be, c.inputs[0])[0]] * len(c.inputs)
+    else:
+        ins = [materialize(be, a)[0] for a in c.inputs]
     p = c.kparams()
     if c.op == "transpose":
         # forward is metadata-only; the interesting part is the backward accumulate
@@ -264,6 +352,8 @@ def run_case(be: Backend, c: Case) -> dict:
         be.fwd("transpose", ins, out, p)
         g = np.random.RandomState(c.dout_seed).randn(*c.out_shape).astype(np.float32)
         be.set_grad(out, g)
+        if c.grad_init is not None:
+            be.set_grad(ins[0], grad_init_values(c, 0, be.grad_size(ins[0])))
         be.bwd("transpose", ins, out, p)
         res["grad0"] = be.read_grad(ins[0])
         return res
@@ -273,8 +363,12 @@ def run_case(be: Backend, c: Case) -> dict:
     if c.kind == "bwd":
         g = np.random.RandomState(c.dout_seed).randn(*res["out"].shape).astype(np.float32)
         be.set_grad(out, g)
+        if c.grad_init is not None:
+            for k, a in enumerate(c.inputs[:1] if c.same_input else c.inputs):
+                if a.requires_grad:
+                    be.set_grad(ins[k], grad_init_values(c, k, be.grad_size(ins[k])))
         be.bwd(c.op, ins, out, p)
-        for k, a in enumerate(c.inputs):
+        for k, a in enumerate(c.inputs[:1] if c.same_input else c.inputs):
             if a.requires_grad:
                 res[f"grad{k}"] = be.read_grad(ins[k])
     return res

@@ -1,6 +1,6 @@
-"""Tapes that exercise every case of the chain compiler's code generator (shared by the CPU source
-checks and the GPU parity tests): each op, each operand source, both operand orders of SUB/DIV,
-broadcast scalar inputs, and config 2's chain."""
+"""Tapes that exercise every case of the fused-chain interpreter (shared by the GPU parity tests):
+each op, each operand source, both operand orders of SUB/DIV, broadcast scalar inputs, the longest
+tape, and config 2's chain."""
 from __future__ import annotations
 
 from plast_amd.abi import SRC_ACC, SRC_IMM, SRC_INPUT, SRC_NONE

@@ -20,11 +20,16 @@ class DeviceBackend(Backend):
         self.keep.append(t)
         return t
 
-    def view(self, base, shape, strides):
+    def view(self, base, shape, strides, own_grad=False):
         v = DeviceTensor(shape, base.dtype, base=base, strides=strides, zero=False)
         v.t.requires_grad = base.t.requires_grad
         if base.grad is not None:
-            g = DeviceTensor(shape, base.dtype, base=base.grad, strides=strides, zero=False)
+            if own_grad:
+                # a zero-filled gradient of its own, contiguous in the view's shape
+                g = DeviceTensor(shape, base.dtype, zero=True)
+            else:
+                g = DeviceTensor(shape, base.dtype, base=base.grad, strides=strides, zero=False)
+            self.keep.append(g)
             v.grad = g
             v.t.grad = C.pointer(g.t)
         self.keep.append(v)
@@ -49,8 +54,12 @@ class DeviceBackend(Backend):
 
     def set_grad(self, t, arr):
         a = np.ascontiguousarray(arr, dtype=np.float32)
+        assert a.size == self.grad_size(t), "set_grad writes the whole gradient buffer"
         lib().arena_memcpy_h2d_hip(t.grad.ptr, a.ctypes.data, a.nbytes)
         lib().check("set_grad")
+
+    def grad_size(self, t):
+        return int(np.prod(t.grad.shape))
 
 
 def ulp_distance(x: np.ndarray, y: np.ndarray) -> np.ndarray:

@@ -141,12 +141,16 @@ class HostBackend(Backend):
         self.keep.append(t)
         return t
 
-    def view(self, base, shape, strides):
+    def view(self, base, shape, strides, own_grad=False):
         v = HostTensor(base=base, shape=shape, strides=strides)
         v.t.requires_grad = base.t.requires_grad
         if base.grad is not None:
-            # the view's gradient aliases the base gradient with the view's strides
-            g = HostTensor(base=base.grad, shape=shape, strides=strides)
+            if own_grad:
+                # a zero-filled gradient of its own, contiguous in the view's shape
+                g = HostTensor(np.zeros(shape, np.float32))
+            else:
+                # the view's gradient aliases the base gradient with the view's strides
+                g = HostTensor(base=base.grad, shape=shape, strides=strides)
             v.grad = g
             v.t.grad = C.pointer(g.t)
         self.keep.append(v)
@@ -173,6 +177,9 @@ class HostBackend(Backend):
 
     def set_grad(self, t, arr):
         t.grad.buf[:] = np.ascontiguousarray(arr, dtype=t.grad.buf.dtype).reshape(-1)
+
+    def grad_size(self, t):
+        return int(t.grad.buf.size)
 
 
 def ref_ce_chain(logits: np.ndarray, labels: np.ndarray, which: str = "ref", backward: bool = True):

@@ -5,9 +5,9 @@ reference's CPU kernels do (unary_ops.c:8-93). Every result must lie within 2 ul
 counts as equal). The host's glibc version is printed with the result. Measured on MI355X against
 glibc 2.35: worst case 1 ulp for exp, 2 ulp for log, sin, cos and tan.
 
-The same sweep runs through a one-instruction fused chain ([LOAD, op]) as well: at 2^28 elements
-the chain is compiled at run time (a separate compilation of the same ocml functions), so this
-pins the compiled chains' math to glibc too, not only to the interpreter."""
+The same sweep runs through a one-instruction fused chain ([LOAD, op]) as well: the tape
+interpreter's streaming form instantiates the same ocml functions in another kernel, so this pins
+the fused chains' math to glibc too."""
 from __future__ import annotations
 
 import concurrent.futures as cf
@@ -42,7 +42,6 @@ def test_every_float32_within_2_ulp_of_glibc(name, path):
     L = rt.lib()
     print(f"{name} ({path}): all 2^32 inputs against {' '.join(platform.libc_ver())}", flush=True)
     tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), (name.upper(), 0, 0, 0, 0.0)], 1)
-    launches = L.plast_hip_chain_jit_launches()
     worst, bad, example = 0.0, 0, None
     base = np.arange(CHUNK, dtype=np.uint32)
     with cf.ThreadPoolExecutor(max_workers=16) as pool:
@@ -68,5 +67,3 @@ def test_every_float32_within_2_ulp_of_glibc(name, path):
             print(f"{name} chunk {c + 1}/16: worst so far {worst:g} ulp, {bad} beyond 2", flush=True)
     assert bad == 0, f"{name}: {bad} inputs beyond 2 ulp; worst {worst:g} ulp at x={example[0]!r}: " \
                      f"gpu {example[1]!r}, glibc {example[2]!r}"
-    if path == "chain":  # every chunk went through the compiled form
-        assert L.plast_hip_chain_jit_launches() - launches == (1 << 32) // CHUNK
