@@ -1,6 +1,8 @@
-"""Host-side wrappers for the two CPU libraries used as checkers: the oracle (oracle/liboracle.so,
-this repository's C restatement) and the compiled reference (oracle/_ref/libplast_ref.so, built
-from /root/reference's own C sources). Both take the same `Tensor` structs as the HIP library."""
+"""Host-side wrappers for the CPU libraries used as checkers: the oracle (oracle/liboracle.so, this
+repository's C restatement), the compiled reference (oracle/_ref/libplast_ref.so, built from
+/root/reference's own C sources with FMA contraction off) and, where it was built, the same sources
+under the reference's own flags (oracle/_ref/libplast_ref_native.so, contraction on). All take the
+same `Tensor` structs as the HIP library."""
 from __future__ import annotations
 
 import ctypes as C
@@ -14,11 +16,13 @@ from plast_amd.abi import CPU, FLOAT32, INT32, INT64, KernelParams, TensorP, Ten
 ROOT = Path(__file__).resolve().parent.parent
 ORACLE_PATH = ROOT / "oracle" / "liboracle.so"
 REF_PATH = ROOT / "oracle" / "_ref" / "libplast_ref.so"
+NATIVE_PATH = ROOT / "oracle" / "_ref" / "libplast_ref_native.so"
 
 _DT = {np.dtype(np.float32): FLOAT32, np.dtype(np.int32): INT32, np.dtype(np.int64): INT64}
 
 _oracle = None
 _ref = None
+_native = None
 
 
 def oracle():
@@ -39,6 +43,17 @@ def ref():
     if _ref is None:
         _ref = C.CDLL(str(REF_PATH))
     return _ref
+
+
+def native_available() -> bool:
+    return NATIVE_PATH.exists()
+
+
+def native():
+    global _native
+    if _native is None:
+        _native = C.CDLL(str(NATIVE_PATH))
+    return _native
 
 
 class HostTensor:
@@ -130,7 +145,8 @@ from cases import Backend  # noqa: E402
 
 
 class HostBackend(Backend):
-    """Runs cases through the oracle ("oracle") or the compiled reference ("ref")."""
+    """Runs cases through the oracle ("oracle"), the compiled reference ("ref") or the reference
+    built with its own flags ("native")."""
 
     def __init__(self, which: str):
         self.which = which
@@ -163,10 +179,18 @@ class HostBackend(Backend):
         return t
 
     def fwd(self, op, ins, out, p):
-        (oracle_forward if self.which == "oracle" else ref_forward)(op, ins, out, p)
+        if self.which == "oracle":
+            oracle_forward(op, ins, out, p)
+        else:
+            _call(ref() if self.which == "ref" else native(), f"{op}_cpu_forward", ins, out,
+                  p or KernelParams(0, 0, 0.0))
 
     def bwd(self, op, ins, out, p):
-        (oracle_backward if self.which == "oracle" else ref_backward)(op, ins, out, p)
+        if self.which == "oracle":
+            oracle_backward(op, ins, out, p)
+        else:
+            _call(ref() if self.which == "ref" else native(), f"{op}_cpu_backward", ins, out,
+                  p or KernelParams(0, 0, 0.0))
 
     def read(self, t):
         return t.numpy()

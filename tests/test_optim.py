@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from cases import assert_bits
-from hostlib import HostTensor, oracle, ref, ref_available
+from hostlib import HostTensor, native, native_available, oracle, ref, ref_available
 from optim_cases import (HYPER, MANY, OVER, SIZES, SPECIAL, SPECIAL_SEED, f64_reference, grads, host_array, initial, make_opt,
                          read_moments)
 from plast_amd import abi
@@ -77,10 +77,10 @@ def _step_fn(lib, kind, prefix):
 _ARENAS = []
 
 
-def _ref_opt(kind):
+def _ref_opt(kind, which="ref"):
     """The reference's own optimizer struct with CPU arenas (its first step allocates m and v in
     them through init(..., zeros): adam.c:29-46)."""
-    L = ref()
+    L = ref() if which == "ref" else native()
     L.arena_create.restype = abi.Arena
     L.arena_create.argtypes = [C.c_uint64, C.c_int]
     opt = make_opt(kind)
@@ -93,15 +93,16 @@ def _ref_opt(kind):
 
 
 def run_host(which, kind, sizes, seed, steps, with_grad=None):
-    """Run `steps` updates through the oracle ("oracle") or the compiled reference ("ref");
-    returns the parameters and, for Adam/AdamW, the moments after the last step."""
+    """Run `steps` updates through the oracle ("oracle"), the compiled reference ("ref") or the
+    reference built with its own flags ("native"); returns the parameters and, for Adam/AdamW, the
+    moments after the last step."""
     with_grad = with_grad or [True] * len(sizes)
     p0 = initial(sizes, seed)
     params = _host_params(p0, with_grad)
     ptrs, keep = abi.tensor_array(*[t.t for t in params])
-    opt = make_opt(kind) if which == "oracle" else _ref_opt(kind)
-    f = _step_fn(oracle() if which == "oracle" else ref(), kind,
-                 "oracle_" if which == "oracle" else "")
+    opt = make_opt(kind) if which == "oracle" else _ref_opt(kind, which)
+    lib = {"oracle": oracle, "ref": ref, "native": native}[which]()
+    f = _step_fn(lib, kind, "oracle_" if which == "oracle" else "")
     for s in range(steps):
         for t, g, w in zip(params, grads(sizes, seed, s), with_grad):
             if w:
@@ -187,3 +188,38 @@ def test_oracle_optimizer_matches_golden_vectors(kind, set_name):
         if mv is not None:
             assert_bits(mv[i][0], g[f"{set_name}@{kind}@m{i}"], f"{kind} m{i}")
             assert_bits(mv[i][1], g[f"{set_name}@{kind}@v{i}"], f"{kind} v{i}")
+
+
+@pytest.mark.skipif(not native_available(),
+                    reason="oracle/_ref/libplast_ref_native.so not built (needs /root/reference)")
+@pytest.mark.parametrize("kind", ["sgd", "adam", "adamw"])
+def test_oracle_optimizer_against_the_natively_built_reference(kind):
+    """Under the reference's own flags GCC contracts the moment updates (b1 * m + (1 - b1) * g, ...)
+    into FMAs, one rounding where the source reads two; the oracle and the HIP path keep the
+    source's roundings. After three steps every value is within 2^-18 (a few ulps per step) of the
+    native build's, measured against the value's magnitude plus the magnitudes it was summed from
+    (values can cancel towards 0): for a parameter its total update, for m the sum of |g| over the
+    steps, for v the sum of g^2. NaN matches NaN; the differing counts are printed. SGD
+    (p -= lr * g) contracts too."""
+    sizes, seed, steps = SIZES, 11, 3
+    p0 = initial(sizes, seed)
+    gs = [grads(sizes, seed, st) for st in range(steps)]
+    po, mvo, _ = run_host("oracle", kind, sizes, seed, steps)
+    pn, mvn, _ = run_host("native", kind, sizes, seed, steps)
+    pairs = [("param", a, b, np.abs(a.astype(np.float64) - x0)) for a, b, x0 in zip(po, pn, p0)]
+    if mvo is not None:
+        for i, ((mo, vo), (mn, vn)) in enumerate(zip(mvo, mvn)):
+            g64 = [g[i].astype(np.float64).reshape(mo.shape) for g in gs]
+            pairs += [("m", mo, mn, sum(np.abs(g) for g in g64)),
+                      ("v", vo, vn, sum(g * g for g in g64))]
+    diff, total = {}, {}
+    for name, a, b, moved in pairs:
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        nan = np.isnan(a64) & np.isnan(b64)
+        tol = 2.0 ** -18 * (np.maximum(np.abs(a64), np.abs(b64)) + moved) + 2.0 ** -149
+        ok = nan | (np.abs(a64 - b64) <= tol)
+        assert ok.all(), f"{kind} {name}: {int((~ok).sum())} beyond the bound"
+        diff[name] = diff.get(name, 0) + int(((a.view(np.uint32) != b.view(np.uint32)) & ~nan).sum())
+        total[name] = total.get(name, 0) + a.size
+    print(f"{kind}: elements differing from the native build after 3 steps: " +
+          ", ".join(f"{k} {diff[k]}/{total[k]}" for k in diff))

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from cases import CASES, assert_bits, assert_close_sum, materialize, run_case
-from hostlib import (HostBackend, HostTensor, fused_chain2, libm_expf, oracle_backward,
+from hostlib import (HostBackend, HostTensor, fused_chain2, libm_expf, native_available, oracle_backward,
                      oracle_forward, ref_available, ref_ce_chain, ref_forward)
 from plast_amd.abi import DIM_ALL, KernelParams
 
@@ -202,3 +202,101 @@ def test_planted_mistake_is_caught():
     bad = run_case(Planted("oracle"), c)
     with pytest.raises(AssertionError):
         assert_bits(bad["out"], good["out"], "planted")
+
+
+EXPAND_CASES = [((3,), (2, 3)), ((1, 3), (4, 3)), ((2, 1, 4), (2, 5, 4)), ((1,), (7,)),
+                ((2, 3), (2, 3)), ((1, 1), (3, 2)), ((4, 1), (2, 4, 6)), ("T", (5, 3, 2))]
+
+
+@pytest.mark.parametrize("a_shape, out_shape", EXPAND_CASES, ids=[str(c) for c in EXPAND_CASES])
+def test_expand_metadata(a_shape, out_shape):
+    """oracle_expand_forward (shape_ops.c:54-57 with cpu_utils.c:59-76) against the compiled
+    reference's expand_cpu_forward and broadcast_cpu_forward, the HIP library's expand and
+    broadcast forwards (host-side metadata, no device needed) and numpy's broadcast_to strides:
+    the output aliases the input's data and gradient, new leading axes and expanded size-1 axes
+    get stride 0, every other axis keeps the input's stride. "T" is a transposed [3, 1] input."""
+    import ctypes as C
+    from plast_amd import abi
+    if a_shape == "T":
+        base = HostTensor(np.arange(3, dtype=np.float32).reshape(1, 3), requires_grad=True)
+        a = HostTensor(base=base, shape=(3, 1), strides=(1, 3))
+        a.grad = base.grad
+        a.t.grad = C.pointer(base.grad.t)
+        a.t.requires_grad = True
+        a_strides = (1, 3)
+    else:
+        a = HostTensor(np.zeros(a_shape, np.float32), requires_grad=True)
+        a_strides = abi.strides_of(a.t)
+    view = np.lib.stride_tricks.as_strided(np.zeros(1, np.float32), shape=a.t.shape[:a.t.ndim],
+                                           strides=[4 * s for s in a_strides])
+    want = tuple(s // 4 for s in np.broadcast_to(view, out_shape).strides)
+    runs = [("oracle", lambda o: oracle_forward("expand", [a], o))]
+    if ref_available():
+        runs += [("ref expand", lambda o: ref_forward("expand", [a], o)),
+                 ("ref broadcast", lambda o: ref_forward("broadcast", [a], o))]
+    from plast_amd.runtime import LIB_PATH
+    hip = C.CDLL(str(LIB_PATH))   # loaded without initialising a device: these calls need none
+    for f in (hip.expand_hip_forward, hip.broadcast_hip_forward):
+        f.argtypes, f.restype = [abi.TensorPP, abi.TensorP, KernelParams], None
+    ins = (abi.TensorP * 1)(C.pointer(a.t))
+    runs += [("hip expand", lambda o: hip.expand_hip_forward(ins, C.byref(o.t), KernelParams(0, 0, 0.0))),
+             ("hip broadcast", lambda o: hip.broadcast_hip_forward(ins, C.byref(o.t),
+                                                                   KernelParams(0, 0, 0.0)))]
+    for name, run in runs:
+        o = HostTensor(np.zeros(out_shape, np.float32))
+        run(o)
+        assert o.t.data == a.t.data, f"{name}: data not aliased"
+        assert C.cast(o.t.grad, C.c_void_p).value == C.cast(a.t.grad, C.c_void_p).value, \
+            f"{name}: grad not shared"
+        assert abi.strides_of(o.t) == want, f"{name}: strides {abi.strides_of(o.t)} != {want}"
+
+
+@pytest.mark.skipif(not native_available(),
+                    reason="oracle/_ref/libplast_ref_native.so not built (needs /root/reference)")
+def test_separate_rounding_against_the_natively_built_reference():
+    """The reference's Makefile:7 flags (-O3 -march=native) leave GCC's FMA contraction on, so that
+    build computes a backward's `da += g * x` as fma(g, x, da): one rounding where the C source reads
+    two. The oracle (and so the HIP path, bit-equal to it) keeps the source's two roundings. Here:
+    every forward output is bit-identical to the native build; every exactly-ordered backward is
+    within 2^-21 * (|increment| + |result|) of it, where increment is what the same backward adds to
+    a zero gradient (one rounding of the product, one of the sum, doubled for two terms into one
+    buffer). From a zero gradient fma(g, x, 0) rounds as g * x, so only a gradient formula with a
+    product inside (tan's 1 + t*t) can differ there. The counts of differing elements are
+    printed."""
+    from cases import Case
+    import dataclasses
+    fwd_same = 0
+    acc_diff, acc_total, worst = {}, {}, 0.0
+    for c in REF_CASES:
+        got = run_case(HostBackend("oracle"), c)
+        nat = run_case(HostBackend("native"), c)
+        if c.kind == "fwd":
+            for k in got:
+                assert_bits(got[k], nat[k], f"{c.id}:{k} forward vs native")
+            fwd_same += 1
+            continue
+        if not c.exact:   # the reference's omp atomics: order unspecified
+            continue
+        start = "zero" if c.grad_init is None and not c.same_input else "acc"
+        zero = run_case(HostBackend("oracle"), dataclasses.replace(c, grad_init=None))
+        for k in got:
+            if not k.startswith("grad"):
+                assert_bits(got[k], nat[k], f"{c.id}:{k}")
+                continue
+            g64, n64 = got[k].astype(np.float64), nat[k].astype(np.float64)
+            bound = 2.0 ** -21 * (np.abs(zero[k].astype(np.float64)) + np.abs(g64)) + 2.0 ** -149
+            d = np.abs(g64 - n64)
+            both_nan = np.isnan(g64) & np.isnan(n64)
+            ok = both_nan | (d <= bound)
+            assert ok.all(), f"{c.id}:{k}: {int((~ok).sum())} beyond the contraction bound"
+            worst = max(worst, float(np.max(np.where(both_nan, 0.0, d / bound))))
+            diff = int(((got[k].view(np.uint32) != nat[k].view(np.uint32)) & ~both_nan).sum())
+            key = (start, c.op)
+            acc_diff[key] = acc_diff.get(key, 0) + diff
+            acc_total[key] = acc_total.get(key, 0) + got[k].size
+    print(f"forward cases bit-identical to the native build: {fwd_same}")
+    for start in ("zero", "acc"):
+        print(f"backward from a {start} gradient, elements differing from the native build: " +
+              ", ".join(f"{op} {acc_diff[(st, op)]}/{acc_total[(st, op)]}"
+                        for st, op in sorted(acc_diff) if st == start))
+    print(f"largest difference as a fraction of the bound: {worst:.3f}")
