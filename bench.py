@@ -341,6 +341,35 @@ class C5(Workload):
             backward("softmax", [self.X], self.Y, KernelParams(1, 0, 0.0))
 
 
+class C5Step(Workload):
+    """Config 5's whole training step in one pass (softmax_cross_entropy_step_hip): logits
+    [32768, 32000] ~ N(0, 2), labels U{0..31999}, dloss = 1/N (the mean's gradient); writes the
+    row statistics and loss, dlogits = dloss * (softmax - onehot) and dbias = sum_rows dlogits.
+    Algorithmic bytes: the logits read once and dlogits written once (8 B/element), labels, dloss,
+    loss (4 B/row each), stats (8 B/row) and dbias (4 B/column); the workgroups' column-sum
+    partials (256 x 32000 x 4 B written and read) are workspace, not counted."""
+    name = "config5_ce_step_one_pass"
+
+    def __init__(self):
+        self.N, self.C = 32768, 32000
+        self.elems = self.N * self.C
+        self.bytes_per_call = 8 * self.elems + 4 * self.N * 3 + 8 * self.N + 4 * self.C
+
+    def setup(self):
+        N, Cn = self.N, self.C
+        self.X = DeviceTensor((N, Cn), zero=False).fill_("normal", 42, 0.0, 2.0)
+        self.lab = DeviceTensor((N,), INT32, zero=False).fill_("randint", 45, 0, Cn)
+        self.g = DeviceTensor((N,), zero=False).fill_("uniform", 7, 1.0 / N, 1.0 / N)
+        self.st = DeviceTensor((N, 2), zero=False)
+        self.loss = DeviceTensor((N,), zero=False)
+        self.dx = DeviceTensor((N, Cn), zero=False)
+        self.db = DeviceTensor((Cn,), zero=False)
+
+    def step(self):
+        lib().softmax_cross_entropy_step_hip(self.X.ptr, self.lab.ptr, self.g.ptr, self.st.ptr,
+                                             self.loss.ptr, self.dx.ptr, self.db.ptr, self.N, self.C)
+
+
 class Optim(Workload):
     """Optimizer row: one step of SGD / Adam / AdamW over `count` fp32 parameters totalling 64M
     elements (gradients ~ N(0, 0.1)), or zero_grad of a 64M gradient. Bytes per element: SGD reads
@@ -485,6 +514,7 @@ def detail_workloads():
         "c5f": C5("fwd"), "c5b": C5("bwd"), "c5bw": C5("bwd_w"), "c5bias": C5("bias"),
         "c5softmax": C5("softmax"), "c5softmaxb": C5("softmax_bwd"),
         "c5max": C5("op_max"), "c5exp": C5("op_exp"), "c5sum": C5("op_sum"),
+        "c5step": C5Step(),
         "optsgd": Optim("sgd"), "optadam": Optim("adam"), "optadamw": Optim("adamw"),
         "optadam512": Optim("adam", 512), "zerograd": Optim("zero_grad"),
         "pack": Pack("pack"), "tohost": Pack("host"),

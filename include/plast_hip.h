@@ -183,6 +183,23 @@ void bias_grad_reduce_hip(const float *dc_mod, float *dbias, u64 num_elements, u
 void relu_grad_modulate_bias_grad_hip(const float *dout, const float *out_data, float *dc,
                                       float *dbias, u64 num_elements, u64 cols, float alpha);
 
+/* ------------------------------------------------------------------ cross-entropy step ------- */
+
+/* One pass of a cross-entropy training step over row-major [N, C] fp32 logits with int32 labels
+ * [N]: the forward of softmax_cross_entropy_hip_forward (stats [N, 2] = row max and log of the
+ * exp-sum, loss [N] per row), its backward dlogits = dloss[i] * (softmax - onehot) written (not
+ * accumulated), and, when dbias is not NULL, dbias[c] = sum over rows of dlogits[., c] written:
+ * the gradient of a bias broadcast-added to the logits (the reference's ADD backward into a [C]
+ * operand, kernel_macros.h:283-299). dloss [N] is the upstream gradient of each row's loss (1/N
+ * for a mean), known before the step. Each logit is read once and each gradient written once
+ * (rows of whole float4 up to 32768 floats; other rows run the three passes). No counterpart in
+ * the reference, which runs the op chain of src/api/loss.c:97-169, its backward and the bias's
+ * ADD backward as separate passes; for callers that train with a cross-entropy loss. All pointers
+ * are device memory; returns after the work completes (or is queued, in asynchronous mode). */
+void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, const float *dloss,
+                                    float *stats, float *loss, float *dlogits, float *dbias, u64 N,
+                                    u64 C);
+
 /* ------------------------------------------------------------------ pack / host transfer ----- */
 
 /* A contiguous image of a possibly strided tensor, layout-identical to CudaTensorPack

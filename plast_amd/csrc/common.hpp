@@ -66,6 +66,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_TAPE_SUNROLL
 #define PLAST_TAPE_SUNROLL 1
 #endif
+#ifndef PLAST_TAPE_SMODE
+#define PLAST_TAPE_SMODE 0  // 0: grid-stride steps, 1: a contiguous range of steps per workgroup
+#endif
 #ifndef PLAST_TAPE_TILE_ROWS
 #define PLAST_TAPE_TILE_ROWS 2  // fused chains in the transposed-operand tile: rows per evaluation
 #endif
@@ -168,6 +171,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 #ifndef PLAST_CE_BWD_BLOCK
 #define PLAST_CE_BWD_BLOCK 256  // cross-entropy backward, flat form: workgroup size
+#endif
+#ifndef PLAST_CE_STEP_BLOCK
+#define PLAST_CE_STEP_BLOCK 512  // one-pass cross-entropy step: lanes per workgroup (one row)
+#endif
+#ifndef PLAST_CE_STEP_WPC
+#define PLAST_CE_STEP_WPC 1  // one-pass cross-entropy step: persistent workgroups per CU
 #endif
 #ifndef PLAST_CE_BWD_UNROLL
 #define PLAST_CE_BWD_UNROLL 1  // float4 units per lane, cross-entropy backward

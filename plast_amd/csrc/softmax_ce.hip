@@ -39,6 +39,18 @@ __device__ __forceinline__ float exp_le0(float t) {
   return t < -87.0f ? 0.0f : e;
 }
 
+// exp_le0 without the range clamp, for finite t <= 0 only (-inf would give NaN): below t = -87 it
+// returns the subnormal or zero that 2^p gives. Two instructions fewer.
+__device__ __forceinline__ float exp_le0_finite(float t) {
+  constexpr float kL = 1.44269502162933349609375f;
+  constexpr float kLlo = 1.925963033500011079e-8f;
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float p = t * kL;
+  const float d = __builtin_fmaf(t, kLlo, __builtin_fmaf(t, kL, -p));
+  const float r = __builtin_amdgcn_exp2f(p);
+  return __builtin_fmaf(r, d * kLn2, r);
+}
+
 // Block-wide reductions over W waves (lds holds W + 1 floats), combined in wave order.
 template <int W = kCeWaves>
 __device__ __forceinline__ float block_sum(float v, float *lds) {
@@ -379,6 +391,273 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
     const float gv = g * (sm - oh);
     dr[j] = OVERWRITE ? gv : dr[j] + gv;
   }
+}
+
+// ---- a whole cross-entropy training step in one pass: the forward's row statistics and loss,
+// the backward's dx = dloss * (softmax - onehot), and the bias gradient sum_rows dx, reading each
+// logit once and writing each gradient once. Persistent workgroups of kStepBlock lanes walk rows
+// b, b + G, b + 2G, ...; a row is held in registers (V float4 per lane; lanes past the row are
+// masked), and the next row's loads are issued into a second register set before the current row is
+// reduced, so memory keeps streaming through the row's two block reductions. Per row, with the
+// forward kernel's semantics (ce_fwd_wave_kernel): M = the block max, S = sum exp(x - M) in the
+// block's fixed order, l = logf(S); rows whose fast values could differ from the reference chain's
+// bits (a non-finite S or M, a zero M, an overflowing shifted-normalised logit) are recomputed
+// exactly from memory. Each lane adds the dx of its columns into the workgroup's column sums in LDS
+// (a slot per lane and unit; a lane only ever touches its own slots, so no synchronisation is
+// needed) across the
+// workgroup's rows; at the end the workgroup writes them to part[b][C], and ce_step_finalize adds
+// the G rows of part in workgroup order. No atomics: the bias gradient is deterministic for a
+// given grid. Registers hold the two row sets only (the column sums there would spill at 1024
+// lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
+constexpr int kStepBlock = PLAST_CE_STEP_BLOCK;
+
+// Exact row statistics for the rare rows the fast path cannot take: the reference's serial max
+// fold, then the exp-sum with expf and the "some other term is non-finite" flag of the one-hot
+// product (the whole block takes this branch).
+template <int W>
+__device__ void ce_row_exact(const float *row, uint32_t C, int32_t y, float *lds, float &mx,
+                             float &l, bool &bad) {
+  constexpr int BS = W * 64;
+  __syncthreads();
+  if (threadIdx.x == 0) lds[W] = serial_max_fold(row, C);
+  __syncthreads();
+  mx = lds[W];
+  float t = 0.0f;
+  for (uint32_t j = threadIdx.x; j < C; j += BS) t += expf(row[j] - mx);
+  l = logf(block_sum<W>(t, lds));
+  bool b = false;
+  for (uint32_t j = threadIdx.x; j < C; j += BS) {
+    const float ls = (row[j] - mx) - l;
+    if (int32_t(j) != y) b = b || !(fabsf(ls) <= FLT_MAX);
+  }
+  bad = block_any<W>(b, lds);
+}
+
+template <int V>
+__global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
+    const float *__restrict__ x, const int32_t *__restrict__ lab, const float *__restrict__ dloss,
+    float *__restrict__ stats, float *__restrict__ loss, float *__restrict__ dx,
+    float *__restrict__ part, uint32_t N, uint32_t C, uint32_t simd_end) {
+  constexpr int BS = kStepBlock, W = BS / 64;
+  // one area per reduction round of a row: a round's single barrier orders its writes after every
+  // read of the same area in the previous row (which precede the other round's barrier)
+  __shared__ float red1[2 * W], red2[W], ex[W + 2];
+  extern __shared__ f4 colsum[];  // BS * V float4: the workgroup's column sums, then padding
+  const uint32_t C4 = C / 4, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // row indices are 32-bit (the host checks N < 2^32): a 64-bit bound compare would be made in
+  // vector registers, which the loop head may find still tied to an in-flight memory operation
+  const uint32_t G = gridDim.x;
+  const float ninf = -__builtin_huge_valf(), pinf = __builtin_huge_valf();
+#pragma unroll
+  for (int u = 0; u < V; ++u) colsum[t + uint32_t(u) * BS] = f4(0.0f);
+
+  // The lane index is made opaque in each row step, so the per-unit offsets and masks derived
+  // from it are recomputed there (a few adds) instead of being hoisted out of the row loop, where
+  // they would be spilled to scratch at this register budget.
+  auto lane_index = [&]() {
+    uint32_t i = t;
+    asm volatile("" : "+v"(i));
+    return i;
+  };
+  // Every load is issued unconditionally (a lane past the row reads the row's last float4, and the
+  // prefetch past the last row re-reads that row): a load under a branch may not have been issued,
+  // so the wait before the current row's first use could not count the prefetch as outstanding and
+  // would wait for it too. Lanes past the row are masked where their values are used.
+  auto load_row = [&](uint32_t r, f4 (&v)[V]) {
+    const f4 *x4 = reinterpret_cast<const f4 *>(x + uint64_t(r < N ? r : N - 1) * C);
+    const uint32_t ti = lane_index();
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+      const uint32_t q = ti + uint32_t(u) * BS;
+      v[u] = __builtin_nontemporal_load(x4 + (q < C4 ? q : C4 - 1));
+    }
+  };
+
+  // One row held in v: v is overwritten with e = exp(x - M) by the sum pass, so the gradient
+  // pass is one multiply per element, dx = e * (dloss / S) (the softmax exp((x - m) - l) as
+  // e / S, within 2 ulp of it), with the one-hot term applied to the label's element alone. A
+  // row's VALU work is then about 14 instructions per element, under the memory time (the
+  // recomputed-exponential form took 36 and was issue-bound).
+  auto process = [&](uint32_t r, f4 (&v)[V]) {
+    // Consume every unit of the row here, on every path: a unit used only under a branch that some
+    // waves skip (the row's ragged last unit) would leave its load pending past the loop's back
+    // edge, and reusing its registers there would wait for every load, the prefetch included.
+#pragma unroll
+    for (int u = 0; u < V; ++u) asm volatile("" ::"v"(v[u][0]), "v"(v[u][1]), "v"(v[u][2]), "v"(v[u][3]));
+    const float g = dloss[r];
+    const int32_t y = lab[r];
+    const uint32_t ti = lane_index();
+    const uint32_t full = C4 / BS;  // units every lane holds inside the row
+    // round 1: the row's max and min (lanes past the row hold a copy of its last float4, which
+    // changes neither)
+    float m = ninf, mn = pinf;
+#pragma unroll
+    for (int u = 0; u < V; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        m = fmaxf(m, v[u][c]);
+        mn = fminf(mn, v[u][c]);
+      }
+    m = wave_max(m);
+    mn = wave_min(mn);
+    if (lane == 0) {
+      red1[wave] = m;
+      red1[W + wave] = mn;
+    }
+    // the label's logit, taken by the lane that holds it before the sum pass overwrites v
+    const bool live = y >= 0 && uint32_t(y) < C;
+    const uint32_t yq = live ? uint32_t(y) >> 2 : 0;
+    const bool owner = ti == yq % BS;
+    float xy = 0.0f;
+    if (owner) {
+#pragma unroll
+      for (int u = 0; u < V; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (uint32_t(u) == yq / BS && c == int(y & 3)) xy = v[u][c];
+    }
+    __syncthreads();
+    float M = red1[0], MN = red1[W];
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      M = fmaxf(M, red1[w]);
+      MN = fminf(MN, red1[W + w]);
+    }
+    // round 2: e = exp(x - M) into v, and its sum. A NaN logit reaches the sum; an infinite one,
+    // or an x - M that overflows, sends the row to the exact path below, so every value used from
+    // here on came from a finite argument and the unclamped exponential is exact enough.
+    float sl = 0.0f;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+      const bool in = uint32_t(u) < full || ti + uint32_t(u) * BS < C4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float e = exp_le0_finite(v[u][c] - M);
+        v[u][c] = e;
+        sl += in ? e : 0.0f;
+      }
+    }
+    sl = wave_sum(sl);
+    if (lane == 0) red2[wave] = sl;
+    __syncthreads();
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) S += red2[w];
+    float mx = M, l = 0.0f;
+    bool exact = !(fabsf(M) <= FLT_MAX) || M == 0.0f || !(S <= FLT_MAX);
+    if (!exact) {
+      l = logf(S);
+      // the most negative shifted-normalised logit must stay finite (else 0 * -inf = NaN)
+      exact = !(fabsf((MN - mx) - l) <= FLT_MAX);
+    }
+    bool bad = false;
+    if (exact) ce_row_exact<W>(x + uint64_t(r) * C, C, y, ex, mx, l, bad);
+    // the lane holding the label's logit writes the loss and the statistics
+    if (owner) {
+      float tt = 0.0f;
+      if (bad) tt = __builtin_nanf("");
+      else if (live) tt = 0.0f + ((xy - mx) - l);
+      loss[r] = r < simd_end ? 0.0f - tt : -tt;
+      stats[2 * uint64_t(r)] = mx;
+      stats[2 * uint64_t(r) + 1] = l;
+    }
+    // the gradient, written once and added into the lane's column sums
+    f4 *d4 = reinterpret_cast<f4 *>(dx + uint64_t(r) * C);
+    if (!exact) {
+      const float gs = g * (1.0f / S);
+      const float inv = 1.0f / S;
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const uint32_t q = ti + uint32_t(u) * BS;
+        f4 o = v[u] * gs;
+        if (owner && uint32_t(u) == yq / BS && live) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (c == int(y & 3)) o[c] = g * (v[u][c] * inv - 1.0f);
+        }
+        colsum[q] = colsum[q] + o;  // lanes past the row add into padding slots
+        if (uint32_t(u) < full || q < C4) store_stream<PLAST_CE_NT_STORE>(o, d4 + q);
+      }
+    } else {
+      // the exact statistics: the gradient from memory, as the backward op computes it
+      const f4 *x4 = reinterpret_cast<const f4 *>(x + uint64_t(r) * C);
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const uint32_t q = ti + uint32_t(u) * BS;
+        if (q >= C4) continue;
+        const f4 xv = x4[q];
+        f4 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float sm = exp_le0((xv[c] - mx) - l);
+          const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
+          o[c] = g * (sm - oh);
+        }
+        colsum[q] = colsum[q] + o;
+        store_stream<PLAST_CE_NT_STORE>(o, d4 + q);
+      }
+    }
+  };
+
+  // Two register sets used in turn (a copy out of a set whose loads are in flight would wait for
+  // them), each reloaded right after its row is processed, so one row is always in flight and the
+  // youngest memory operations at the loop's back edge are loads: the loop head may reuse a
+  // register a store of the previous row still reads, and that wait then leaves the prefetch alone
+  // (with the stores last, it would wait for every load too).
+  f4 xa[V], xb[V];
+  uint32_t r = blockIdx.x;
+  load_row(r, xa);
+  load_row(r + G, xb);
+  for (; r < N; r += 2 * G) {
+    process(r, xa);
+    load_row(r + 2 * G, xa);
+    if (r + G >= N) break;
+    process(r + G, xb);
+    load_row(r + 3 * G, xb);
+  }
+  f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(blockIdx.x) * C);
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t q = t + uint32_t(u) * BS;
+    if (q < C4) p4[q] = colsum[q];
+  }
+}
+
+// dbias[c] = sum over workgroups b = 0 .. G-1 of part[b][c], in that order, one lane per column
+// with the loads of each batch of 16 issued before their adds.
+__global__ __launch_bounds__(kCeBlock) void ce_step_finalize(const float *__restrict__ part,
+                                                             float *__restrict__ dbias, uint32_t C,
+                                                             uint32_t G) {
+  const uint32_t c = blockIdx.x * kCeBlock + threadIdx.x;
+  if (c >= C) return;
+  float s = 0.0f;
+  for (uint32_t b0 = 0; b0 < G; b0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = b0 + k < G ? part[uint64_t(b0 + k) * C + c] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (b0 + k < G) s += v[k];
+  }
+  dbias[c] = s;
+}
+
+// Whether ce_step_kernel<V> may be launched with `bytes` of dynamic LDS (raising its limit once:
+// beyond the default the kernel has to opt in).
+bool ce_step_lds_ok(int V, size_t bytes) {
+  static size_t granted[17] = {};
+  if (bytes <= granted[V]) return true;
+  const void *f = V == 1 ? reinterpret_cast<const void *>(&ce_step_kernel<1>)
+                  : V == 2 ? reinterpret_cast<const void *>(&ce_step_kernel<2>)
+                  : V == 4 ? reinterpret_cast<const void *>(&ce_step_kernel<4>)
+                  : V == 8 ? reinterpret_cast<const void *>(&ce_step_kernel<8>)
+                           : reinterpret_cast<const void *>(&ce_step_kernel<16>);
+  if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess) {
+    (void)hipGetLastError();  // not an error of the call: the caller takes the three passes
+    return false;
+  }
+  granted[V] = bytes;
+  return true;
 }
 
 bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
@@ -736,6 +1015,80 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
     else
       ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
   }
+  finish(where);
+}
+
+void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, const float *dloss,
+                                    float *stats, float *loss, float *dlogits, float *dbias, u64 N,
+                                    u64 C) {
+  const char *where = "softmax_cross_entropy_step_hip";
+  if (!ensure_init()) return;
+  if (N == 0) return;
+  if (!logits || !labels || !dloss || !stats || !loss || !dlogits) {
+    report_error(where, "logits, labels, dloss, stats, loss and dlogits are required");
+    return;
+  }
+  if (C == 0 || C >= (uint64_t(1) << 31)) {
+    report_error(where, "rows of %llu elements are not supported", (unsigned long long)C);
+    return;
+  }
+  if (N >= (uint64_t(1) << 31)) {
+    report_error(where, "more than 2^31 rows are not supported (%llu)", (unsigned long long)N);
+    return;
+  }
+  const uint32_t c32 = uint32_t(C);
+  // float4 units per lane for a register-resident row (0: not this kernel)
+  int V = 0;
+  if (C % 4 == 0 && aligned16(logits) && aligned16(dlogits))
+    for (int v = 1; v <= 16 && !V; v *= 2)
+      if (C <= uint64_t(kStepBlock) * 4 * v) V = v;
+  // the column sums live in LDS (one float4 slot per lane and unit, the row's plus padding): the
+  // kernel must be allowed that much of it
+  const size_t lds = size_t(kStepBlock) * size_t(V) * sizeof(f4);
+  if (V && !ce_step_lds_ok(V, lds)) V = 0;
+  if (!V) {
+    // any other row: the forward, the overwriting backward and the column sum as three passes
+    Tensor tx, tl, ts, to, tg, tdx;
+    memset(&tx, 0, sizeof tx);
+    tx.ndim = 2;
+    tx.shape[0] = N, tx.shape[1] = C, tx.strides[0] = C, tx.strides[1] = 1;
+    tx.data = const_cast<float *>(logits), tx.dtype = FLOAT32, tx.device = GPU;
+    tx.requires_grad = true;
+    tdx = tx;
+    tdx.data = dlogits, tdx.requires_grad = false;
+    tx.grad = &tdx;
+    tl = tx;
+    tl.ndim = 1, tl.shape[0] = N, tl.strides[0] = 1, tl.data = const_cast<int32_t *>(labels);
+    tl.dtype = INT32, tl.requires_grad = false, tl.grad = nullptr;
+    ts = tl;
+    ts.shape[0] = 2 * N, ts.data = stats, ts.dtype = FLOAT32;
+    to = tl;
+    to.data = loss, to.dtype = FLOAT32;
+    tg = to;
+    tg.data = const_cast<float *>(dloss);
+    to.grad = &tg;
+    const Tensor *fin[3] = {&tx, &tl, &ts};
+    softmax_cross_entropy_hip_forward(fin, &to, KernelParams{0, 0, 0.0f});
+    Tensor *bin[3] = {&tx, &tl, &ts};
+    softmax_cross_entropy_hip_backward(bin, &to, KernelParams{0, 1, 0.0f});
+    if (dbias) bias_grad_reduce_hip(dlogits, dbias, N * C, C);
+    return;
+  }
+  const uint64_t grid = N < uint64_t(num_cus()) * PLAST_CE_STEP_WPC ? N
+                                                                     : uint64_t(num_cus()) * PLAST_CE_STEP_WPC;
+  // the workgroups' column sums (written even when no bias gradient is wanted; then unread)
+  float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
+  if (!part) return;
+  const uint64_t se = simd_end(N);
+  switch (V) {
+  case 1: ce_step_kernel<1><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
+  case 2: ce_step_kernel<2><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
+  case 4: ce_step_kernel<4><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
+  case 8: ce_step_kernel<8><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
+  default: ce_step_kernel<16><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
+  }
+  if (dbias)
+    ce_step_finalize<<<ceil_div(C, kCeBlock), kCeBlock, 0, stream()>>>(part, dbias, c32, unsigned(grid));
   finish(where);
 }
 
