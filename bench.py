@@ -2,12 +2,15 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c4r,...] [--no-cpu]
 
-Prints ONE JSON line. `value` is config 2: the scheduler-fused
-y = exp(-relu(a*b + c)) over 64M fp32, as achieved HBM GB/s (algorithmic bytes / time). Inputs are
-resident in HBM before timing. Every other config is measured in `detail` with its own GB/s,
-fraction of the 8 TB/s peak and elements/s. The CPU baseline is the reference's own CPU path
-(oracle/_ref/libplast_ref.so, compiled from the reference's sources) on a bounded sample of the same
-workload, on this host's cores.
+Prints ONE JSON line. `value` is config 5 (the largest single-GPU
+config): a whole softmax-cross-entropy training step over [32768, 32000] fp32 logits - the forward's
+row max, log-sum-exp and loss, the backward (softmax - onehot)/N and the bias gradient (the sum over
+rows of that gradient) - as achieved HBM GB/s (algorithmic bytes / time) through the one-pass step
+entry point. Inputs are resident in HBM before timing. Every other config (and config 5 as three
+separate passes) is measured in `detail` with its own GB/s, fraction of the 8 TB/s peak and
+elements/s. The CPU baselines are the reference's own CPU kernels (oracle/_ref/libplast_ref.so,
+compiled from the reference's sources; OpenMP on this host's online cores, whose count is reported)
+on bounded samples of the same workloads.
 """
 from __future__ import annotations
 
@@ -120,6 +123,14 @@ class C2Fused(Workload):
         got = self.y.numpy()[:k]
         ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
         return int(ulp.max())
+
+    def cpu_from(self, head_inputs=None, budget_s=6.0):
+        """The CPU baseline of config 2 for the detail block: its own inputs, generated here."""
+        self.setup()
+        try:
+            return self.cpu(budget_s=budget_s, min_reps=2)
+        finally:
+            self.free()
 
     def cpu(self, budget_s=10.0, min_reps=3):
         """The reference's unfused chain (MUL, ADD, LEAKY_RELU, NEG, EXP) through its CPU kernels,
@@ -502,11 +513,128 @@ class Copy(Workload):
         lib().plast_hip_copy(self.dst.ptr, self.src.ptr, self.elems)
 
 
+# ----------------------------------------------------------------------------- CPU baselines
+def host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _cpu_lib():
+    """(kind, forward, backward, HostTensor) for the reference's compiled CPU kernels, or the
+    oracle's restatement where the reference was not built."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import hostlib
+    if hostlib.ref_available():
+        return "reference", hostlib.ref_forward, hostlib.ref_backward, hostlib.HostTensor
+    return "port", hostlib.oracle_forward, hostlib.oracle_backward, hostlib.HostTensor
+
+
+def _repeat(fn, budget_s, min_reps=2):
+    """Median seconds of fn over repetitions filling about budget_s (at least min_reps)."""
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times), time.perf_counter() - t_start
+
+
+def cpu_config5(X, lab, budget_s=12.0, rows=256):
+    """The reference's cross-entropy step on the host: the op chain of src/api/loss.c:97-169 (MAX,
+    SUB, EXP, SUM, LOG, SUB, MUL one-hot, SUM, NEG, MEAN), its backward in reverse node order, and
+    the bias gradient through its ADD backward (kernel_macros.h:283-299, omp atomics into [C]),
+    over row chunks of the same logits (a full [32768, 32000] chain needs ~10 x 4 GiB of
+    intermediates)."""
+    kind, fwd, bwd, HT = _cpu_lib()
+    sys.path.insert(0, str(ROOT / "tests"))
+    import hostlib
+    N, Cn = X.shape
+    chunks = []
+    for k in range(4):          # four row chunks spread over the logits, read back once
+        r0 = (k * N // 4) // rows * rows
+        chunks.append((X.rows_numpy(r0, rows), lab.numpy()[r0:r0 + rows]))
+    which = "ref" if kind == "reference" else "oracle"
+    state = {"i": 0}
+
+    def one():
+        x, y = chunks[state["i"] % len(chunks)]
+        state["i"] += 1
+        *_, dx = hostlib.ref_ce_chain(x, y, which, backward=True)
+        z = HT(x)
+        b = HT(np.zeros(Cn, np.float32), requires_grad=True)
+        out = HT(np.zeros((rows, Cn), np.float32), requires_grad=True)
+        out.grad.buf[:] = dx.reshape(-1)
+        bwd("add", [z, b], out)
+
+    med, reps, spent = _repeat(one, budget_s)
+    per_row = med / rows
+    bytes_per_row = 8 * Cn + 20
+    return {"value": round(bytes_per_row / per_row / 1e9, 3), "unit": "GB/s", "kind": kind,
+            "ms_full_step": round(per_row * N * 1e3, 1), "rows_per_s": round(1 / per_row, 1),
+            "sample": f"{reps} chunks of {rows} rows x {Cn} of the same logits in {spent:.1f} s, "
+                      f"median; GB/s counts the one-pass step's algorithmic bytes per row "
+                      f"({bytes_per_row} B); ms_full_step extrapolates to {N} rows"}
+
+
+def cpu_config1(budget_s=3.0):
+    """relu(X + b) (ADD's broadcast path: omp; LEAKY_RELU: one thread) and grad_b = SUM over axis
+    0 (the dim reduction: omp over outputs) on the full [1024, 256] config."""
+    kind, fwd, bwd, HT = _cpu_lib()
+    rng = np.random.RandomState(42)
+    X = HT(rng.uniform(-1, 1, (1024, 256)).astype(np.float32))
+    b = HT(rng.uniform(-1, 1, 256).astype(np.float32))
+    gy = HT(rng.uniform(-1, 1, (1024, 256)).astype(np.float32))
+    S, Y, gb = (HT(np.zeros(s, np.float32)) for s in ((1024, 256), (1024, 256), (256,)))
+    f_ms, _, _ = _repeat(lambda: (fwd("add", [X, b], S),
+                                  fwd("leaky_relu", [S], Y, KernelParams(0, 0, 0.0))), budget_s / 2, 20)
+    b_ms, _, _ = _repeat(lambda: fwd("sum", [gy], gb, KernelParams(0, 0, 0.0)), budget_s / 2, 20)
+    return {"fwd_us": round(f_ms * 1e6, 1), "grad_b_us": round(b_ms * 1e6, 1), "kind": kind,
+            "sample": "full config-1 shapes, median of repeated calls"}
+
+
+def cpu_config3(budget_s=4.0, batches=32):
+    """(permute(A, (0,2,1)) + B) * C through the reference's broadcast binary path (omp over
+    output elements with per-element index math) on the first `batches` of the 256 batches."""
+    kind, fwd, bwd, HT = _cpu_lib()
+    rng = np.random.RandomState(42)
+    base = HT(rng.randn(batches, 512, 512).astype(np.float32))
+    A = HT(base=base, shape=(batches, 512, 512), strides=(262144, 1, 512))
+    B = HT(rng.uniform(0.5, 1.5, (1, 512, 1)).astype(np.float32))
+    Cm = HT(rng.uniform(0.5, 1.5, (batches, 1, 512)).astype(np.float32))
+    T, O = HT(np.zeros((batches, 512, 512), np.float32)), HT(np.zeros((batches, 512, 512), np.float32))
+    med, reps, spent = _repeat(lambda: (fwd("add", [A, B], T), fwd("mul", [T, Cm], O)), budget_s)
+    n = batches * 512 * 512
+    return {"value": round(8 * n / med / 1e9, 3), "unit": "GB/s (fused algorithmic bytes)",
+            "kind": kind, "ms_full": round(med * 256 / batches * 1e3, 1),
+            "sample": f"{batches} of 256 batches, add then mul, {reps} repetitions in {spent:.1f} s"}
+
+
+def cpu_config4(budget_s=4.0, rows=8192, cols0=16384):
+    """SUM and MAX over the last axis of [rows, 4096] (the dim reduction: omp over rows) and over
+    axis 0 of [4096, cols0] (each output walks 4096 rows at a stride of cols0 floats)."""
+    kind, fwd, bwd, HT = _cpu_lib()
+    rng = np.random.RandomState(42)
+    X = HT(rng.randn(rows, 4096).astype(np.float32))
+    XT = HT(rng.randn(4096, cols0).astype(np.float32))
+    r_out, c_out = HT(np.zeros(rows, np.float32)), HT(np.zeros(cols0, np.float32))
+    res = {"kind": kind}
+    for op in ("sum", "max"):
+        med, _, _ = _repeat(lambda: fwd(op, [X], r_out, KernelParams(1, 0, 0.0)), budget_s / 4)
+        res[f"{op}_rows_GB_s"] = round(4 * rows * 4096 / med / 1e9, 3)
+        med, _, _ = _repeat(lambda: fwd(op, [XT], c_out, KernelParams(0, 0, 0.0)), budget_s / 4)
+        res[f"{op}_axis0_GB_s"] = round(4 * 4096 * cols0 / med / 1e9, 3)
+    res["sample"] = f"rows: [{rows}, 4096] of [65536, 4096]; axis 0: [4096, {cols0}] of [4096, 65536]"
+    return res
+
+
 def detail_workloads():
     return {
         "copy": Copy(),
         "c1f": C1("fwd"), "c1b": C1("bwd"), "c1g": C1("graph"), "c1big": C1("big"),
-        "c2u": C2Fused(False),
+        "c2f": C2Fused(True), "c2u": C2Fused(False),
         "c3f": C3("fused"), "c3a": C3("add"), "c3m": C3("mul"),
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),
         "c4argmax": C4("argmax", 1), "c4csum": C4("sum", 0), "c4cmax": C4("max", 0),
@@ -533,6 +661,49 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     return r
 
 
+def check_step(w: "C5Step", rows=64) -> dict:
+    """Bench-side parity of the headline: `rows` sampled rows against the oracle's cross-entropy
+    (row max bit-exact; log-sum-exp, loss and dlogits at 1e-5 relative), and the step's bias
+    gradient against the library's own leading-axis sum of its dlogits (a separate kernel) at
+    1e-5 of sum |dlogits| per column."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from hostlib import HostTensor, oracle_backward, oracle_forward
+    N, Cn = w.N, w.C
+    idx = np.random.RandomState(5).choice(N, rows, replace=False)
+    worst = {"stats_max_bits": 0, "lse": 0.0, "loss": 0.0, "dlogits": 0.0, "dbias": 0.0}
+    st, lo, g = w.st.numpy(), w.loss.numpy(), w.g.numpy()
+    lab = w.lab.numpy()
+    for r in idx:
+        x = w.X.rows_numpy(int(r), 1)
+        hx, hl = HostTensor(x, requires_grad=True), HostTensor(lab[r:r + 1])
+        hs, ho = HostTensor(np.zeros((1, 2), np.float32)), HostTensor(np.zeros(1, np.float32), requires_grad=True)
+        oracle_forward("softmax_cross_entropy", [hx, hl, hs], ho)
+        ho.grad.buf[:] = g[r]
+        oracle_backward("softmax_cross_entropy", [hx, hl, hs], ho)
+        ws = hs.numpy().reshape(2)
+        worst["stats_max_bits"] += int(np.float32(st[r, 0]).view(np.uint32) != np.float32(ws[0]).view(np.uint32))
+        worst["lse"] = max(worst["lse"], abs(float(st[r, 1]) - float(ws[1])) / (abs(float(ws[1])) + 1e-6))
+        worst["loss"] = max(worst["loss"], abs(float(lo[r]) - float(ho.numpy()[0])) /
+                            (abs(float(ho.numpy()[0])) + abs(float(ws[1])) + 1e-6))
+        d = w.dx.rows_numpy(int(r), 1).astype(np.float64)
+        wd = hx.grad.numpy().astype(np.float64)
+        worst["dlogits"] = max(worst["dlogits"], float(np.max(np.abs(d - wd) / (np.abs(wd) + 1e-2 / N))))
+    L = lib()
+    ref_bias = DeviceTensor((Cn,), zero=False)
+    L.bias_grad_reduce_hip(w.dx.ptr, ref_bias.ptr, N * Cn, Cn)
+    L.check("bias sum")
+    db, rb = w.db.numpy().astype(np.float64), ref_bias.numpy().astype(np.float64)
+    ref_bias.free()
+    # sum over rows of |dlogits| per column: with dlogits = g (softmax - onehot) and g = 1/N it is at
+    # most |dbias| + 2 count / N (count: the rows labelled with that column)
+    count = np.bincount(lab, minlength=Cn).astype(np.float64)
+    scale = np.abs(db) + 2.0 * count * float(g.max()) + 1e-30
+    worst["dbias"] = float(np.max(np.abs(db - rb) / scale))
+    worst["ok"] = (worst["stats_max_bits"] == 0 and worst["lse"] <= 1e-5 and worst["loss"] <= 1e-5
+                   and worst["dlogits"] <= 1e-5 and worst["dbias"] <= 1e-5)
+    return worst
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -543,22 +714,26 @@ def main(argv=None) -> int:
     ap.add_argument("--no-detail", action="store_true")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only; run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (no collective or multi-GPU path is "
+              "built); run with --gpus 1", file=sys.stderr)
         return 2
+    cores = host_cores()
+    # the reference's CPU kernels use OpenMP: every online core of this host, stated in the line
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
 
     L = lib()
     L.plast_hip_set_sync(0)  # order on the library stream; timing brackets synchronise
 
-    # ---- headline: config 2 through the scheduler-fused DAG
-    head = C2Fused(True)
+    # ---- headline: config 5's whole training step, one pass
+    head = C5Step()
     head.setup()
-    log(f"config2: DAG after fusion = {head.kinds} ({head.nfused} chain fused)")
     ms = timed(head.step, a.steps, a.warmup)
     gbs = head.bytes_per_call / (ms * 1e-3) / 1e9
-    same = head.check()
-    log(f"config2 fused: {ms:.4f} ms/step, {gbs:.1f} GB/s, parity (first 1M) max ulp = {same}")
-    if same > 2:
-        raise SystemExit(f"bench.py: config 2 output differs from the oracle by {same} ulp")
+    L.plast_hip_synchronize()
+    parity = check_step(head)
+    log(f"config5 step: {ms:.4f} ms/step, {gbs:.1f} GB/s, parity {parity}")
+    if not parity["ok"]:
+        raise SystemExit(f"bench.py: config 5 step differs from the oracle: {parity}")
 
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
@@ -568,14 +743,24 @@ def main(argv=None) -> int:
         except Exception:
             traffic = None
 
-    cpu = None
+    cpu, cpu_detail = None, {}
     if not a.no_cpu:
-        cpu = head.cpu()
-        log(f"cpu baseline: {cpu}")
+        cpu = cpu_config5(head.X, head.lab)
+        cpu["cores"] = int(os.environ["OMP_NUM_THREADS"])
+        log(f"cpu baseline (config 5): {cpu}")
+        for name, fn in (("config1", cpu_config1), ("config3", cpu_config3),
+                         ("config4", cpu_config4)):
+            try:
+                cpu_detail[name] = fn()
+            except Exception as e:  # report, keep going
+                cpu_detail[name] = {"error": str(e)}
+            log(f"cpu baseline ({name}): {cpu_detail[name]}")
+        cpu_detail["config2"] = C2Fused(True).cpu_from(head_inputs=None)
+    head.free()
 
     detail = {}
     if not a.no_detail:
-        keys = [k for k in a.only.split(",") if k] or list(detail_workloads())
+        keys = [k for k in a.only.split(",") if k] or [k for k in detail_workloads() if k != "c5step"]
         for k in keys:
             w = detail_workloads()[k]
             try:
@@ -586,8 +771,16 @@ def main(argv=None) -> int:
                 log(f"{w.name}: ERROR {e}")
             finally:
                 w.free()
-    head_detail = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "parity_first_1M_max_ulp": same,
-                   "launches_per_step": len(head.kinds)}
+        three = [detail.get(n, {}).get("ms") for n in ("config5_softmax_ce_fwd",
+                                                       "config5_ce_bwd_overwrite",
+                                                       "config5_bias_grad_sum_axis0")]
+        if all(isinstance(t, float) for t in three):
+            detail["config5_step_as_three_passes"] = {
+                "ms": round(sum(three), 4), "passes": ["forward", "backward (overwrite)",
+                                                       "bias gradient sum"],
+                "speedup_of_one_pass": round(sum(three) / ms, 3)}
+    head_detail = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "parity": parity,
+                   "launches_per_step": 2, "kernels": ["ce_step_kernel", "ce_step_finalize"]}
 
     line = {
         "metric": METRIC,
@@ -601,15 +794,22 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: on-device counter-based PRNG, a/b/c ~ N(0,1) seeds 42/43/44",
-        "config": {"workload": "config2: y = exp(-relu(a*b + c)), flat [67108864] fp32, "
-                               "scheduler-fused into one launch", "elements": head.N,
+        "data": "synthetic: on-device counter-based PRNG, logits ~ N(0, 2) seed 42, labels "
+                "U{0..31999} seed 45, dloss = 1/N",
+        "config": {"workload": "config5: softmax cross-entropy training step over [32768, 32000] "
+                               "fp32 logits - row max, log-sum-exp, loss, dlogits = (softmax - "
+                               "onehot)/N and the [32000] bias gradient - in one pass "
+                               "(softmax_cross_entropy_step_hip)",
+                   "rows": head.N, "classes": head.C,
                    "algorithmic_bytes_per_step": head.bytes_per_call},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
-        "elems_per_s": round(head.N / (ms * 1e-3), 1),
-        "detail": {"config2_fused": head_detail, **detail},
+        "elems_per_s": round(head.elems / (ms * 1e-3), 1),
+        "detail": {"config5_step_one_pass": head_detail,
+                   "traffic_source": "profiles/traffic.json (FETCH_SIZE + WRITE_SIZE of the "
+                                     "dominant kernel per launch, calibrated on the copy kernel)",
+                   "cpu_baselines": cpu_detail, **detail},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -124,6 +124,14 @@ def lib() -> Library:
     return _LIB
 
 
+def _row_major(shape) -> tuple[int, ...]:
+    st, acc = [], 1
+    for e in reversed(shape):
+        st.append(acc)
+        acc *= e
+    return tuple(reversed(st))
+
+
 class DeviceTensor:
     """A device allocation plus the `Tensor` struct that describes it (host metadata)."""
 
@@ -176,6 +184,18 @@ class DeviceTensor:
         strides = abi.strides_of(self.t)
         return np.lib.stride_tricks.as_strided(
             buf[off:], shape=shape, strides=[s * self.itemsize for s in strides]).copy()
+
+    def rows_numpy(self, r0: int, rows: int) -> np.ndarray:
+        """Rows [r0, r0 + rows) of a contiguous tensor, copied back without the rest."""
+        if self.base is not None or abi.strides_of(self.t) != _row_major(self.shape):
+            raise ValueError("rows_numpy needs a contiguous tensor of its own")
+        row = int(np.prod(self.shape[1:])) if len(self.shape) > 1 else 1
+        out = np.empty((rows,) + self.shape[1:], dtype=_NP_DTYPE[self.dtype])
+        if out.nbytes:
+            lib().arena_memcpy_d2h_hip(out.ctypes.data, self.ptr + r0 * row * self.itemsize,
+                                       out.nbytes)
+            lib().check("d2h")
+        return out
 
     def fill_(self, kind: str, seed: int, a: float, b: float) -> "DeviceTensor":
         L = lib()
