@@ -192,7 +192,7 @@ void relu_grad_modulate_bias_grad_hip(const float *dout, const float *out_data, 
  * the gradient of a bias broadcast-added to the logits (the reference's ADD backward into a [C]
  * operand, kernel_macros.h:283-299). dloss [N] is the upstream gradient of each row's loss (1/N
  * for a mean), known before the step. Each logit is read once and each gradient written once
- * (rows of whole float4 up to 32768 floats; other rows run the three passes). No counterpart in
+ * (16-byte aligned rows of whole float4 up to 32768 floats; other rows run the three passes). No counterpart in
  * the reference, which runs the op chain of src/api/loss.c:97-169, its backward and the bias's
  * ADD backward as separate passes; for callers that train with a cross-entropy loss. All pointers
  * are device memory; returns after the work completes (or is queued, in asynchronous mode). */

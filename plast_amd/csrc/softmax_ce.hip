@@ -410,6 +410,15 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // given grid. Registers hold the two row sets only (the column sums there would spill at 1024
 // lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
 constexpr int kStepBlock = PLAST_CE_STEP_BLOCK;
+// The widest row the LDS column sums allow: a float4 slot per lane and unit within 159 KiB of a
+// CU's 160 (1024 lanes: 8 units, rows up to 32768 floats; 512 lanes: 16 units, 65536 floats).
+constexpr int step_max_units() {
+  int v = 16;
+  while (v > 1 && size_t(kStepBlock) * size_t(v) * 16 > size_t(159) * 1024) v /= 2;
+  return v;
+}
+constexpr int kStepMaxV = step_max_units();
+constexpr uint64_t kStepMaxC = uint64_t(kStepBlock) * 4 * kStepMaxV;
 
 // Exact row statistics for the rare rows the fast path cannot take: the reference's serial max
 // fold, then the exp-sum with expf and the "some other term is non-finite" flag of the one-hot
@@ -463,13 +472,16 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // prefetch past the last row re-reads that row): a load under a branch may not have been issued,
   // so the wait before the current row's first use could not count the prefetch as outstanding and
   // would wait for it too. Lanes past the row are masked where their values are used.
+  // Addresses are a row base (uniform) plus a 32-bit byte offset per lane, which the loads and
+  // stores take in one register (a 64-bit address per unit would take two).
   auto load_row = [&](uint32_t r, f4 (&v)[V]) {
-    const f4 *x4 = reinterpret_cast<const f4 *>(x + uint64_t(r < N ? r : N - 1) * C);
+    const char *xr = reinterpret_cast<const char *>(x + uint64_t(r < N ? r : N - 1) * C);
     const uint32_t ti = lane_index();
 #pragma unroll
     for (int u = 0; u < V; ++u) {
       const uint32_t q = ti + uint32_t(u) * BS;
-      v[u] = __builtin_nontemporal_load(x4 + (q < C4 ? q : C4 - 1));
+      const uint32_t off = (q < C4 ? q : C4 - 1) * 16u;
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + off));
     }
   };
 
@@ -563,6 +575,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     }
     // the gradient, written once and added into the lane's column sums
     f4 *d4 = reinterpret_cast<f4 *>(dx + uint64_t(r) * C);
+    char *dr = reinterpret_cast<char *>(d4);
     if (!exact) {
       const float gs = g * (1.0f / S);
       const float inv = 1.0f / S;
@@ -576,7 +589,8 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
             if (c == int(y & 3)) o[c] = g * (v[u][c] * inv - 1.0f);
         }
         colsum[q] = colsum[q] + o;  // lanes past the row add into padding slots
-        if (uint32_t(u) < full || q < C4) store_stream<PLAST_CE_NT_STORE>(o, d4 + q);
+        if (uint32_t(u) < full || q < C4)
+          store_stream<PLAST_CE_NT_STORE>(o, reinterpret_cast<f4 *>(dr + q * 16u));
       }
     } else {
       // the exact statistics: the gradient from memory, as the backward op computes it
@@ -604,16 +618,34 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // youngest memory operations at the loop's back edge are loads: the loop head may reuse a
   // register a store of the previous row still reads, and that wait then leaves the prefetch alone
   // (with the stores last, it would wait for every load too).
-  f4 xa[V], xb[V];
   uint32_t r = blockIdx.x;
-  load_row(r, xa);
-  load_row(r + G, xb);
-  for (; r < N; r += 2 * G) {
-    process(r, xa);
-    load_row(r + 2 * G, xa);
-    if (r + G >= N) break;
-    process(r + G, xb);
-    load_row(r + 3 * G, xb);
+  if constexpr (PLAST_CE_STEP_SETS == 3) {
+    // three sets: two rows in flight while one is processed
+    f4 xa[V], xb[V], xc[V];
+    load_row(r, xa);
+    load_row(r + G, xb);
+    load_row(r + 2 * G, xc);
+    for (; r < N; r += 3 * G) {
+      process(r, xa);
+      load_row(r + 3 * G, xa);
+      if (r + G >= N) break;
+      process(r + G, xb);
+      load_row(r + 4 * G, xb);
+      if (r + 2 * G >= N) break;
+      process(r + 2 * G, xc);
+      load_row(r + 5 * G, xc);
+    }
+  } else {
+    f4 xa[V], xb[V];
+    load_row(r, xa);
+    load_row(r + G, xb);
+    for (; r < N; r += 2 * G) {
+      process(r, xa);
+      load_row(r + 2 * G, xa);
+      if (r + G >= N) break;
+      process(r + G, xb);
+      load_row(r + 3 * G, xb);
+    }
   }
   f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(blockIdx.x) * C);
 #pragma unroll
@@ -642,22 +674,83 @@ __global__ __launch_bounds__(kCeBlock) void ce_step_finalize(const float *__rest
   dbias[c] = s;
 }
 
-// Whether ce_step_kernel<V> may be launched with `bytes` of dynamic LDS (raising its limit once:
-// beyond the default the kernel has to opt in).
-bool ce_step_lds_ok(int V, size_t bytes) {
-  static size_t granted[17] = {};
-  if (bytes <= granted[V]) return true;
-  const void *f = V == 1 ? reinterpret_cast<const void *>(&ce_step_kernel<1>)
-                  : V == 2 ? reinterpret_cast<const void *>(&ce_step_kernel<2>)
-                  : V == 4 ? reinterpret_cast<const void *>(&ce_step_kernel<4>)
-                  : V == 8 ? reinterpret_cast<const void *>(&ce_step_kernel<8>)
-                           : reinterpret_cast<const void *>(&ce_step_kernel<16>);
-  if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess) {
+// Whether ce_step_kernel<V> may be launched with its dynamic LDS (raising its limit once: beyond
+// the default the kernel has to opt in).
+template <int V>
+bool ce_step_lds_ok() {
+  static bool granted = false;
+  if (granted) return true;
+  const int bytes = kStepBlock * V * int(sizeof(f4));
+  if (hipFuncSetAttribute(reinterpret_cast<const void *>(&ce_step_kernel<V>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
     (void)hipGetLastError();  // not an error of the call: the caller takes the three passes
     return false;
   }
-  granted[V] = bytes;
+  granted = true;
   return true;
+}
+
+// The float4 units per lane for rows of C floats from V up (0: none of this build's kernels).
+template <int V>
+int ce_step_units(uint64_t C) {
+  if constexpr (V > kStepMaxV) {
+    return 0;
+  } else {
+    if (C <= uint64_t(kStepBlock) * 4 * V) return ce_step_lds_ok<V>() ? V : 0;
+    return ce_step_units<V * 2>(C);
+  }
+}
+
+// The one-pass step with V units per lane over `grid` workgroups, their column sums in
+// part[grid][C].
+template <int V>
+void ce_step_launch_v(int want, unsigned grid, float *part, const float *logits,
+                      const int32_t *labels, const float *dloss, float *stats, float *loss,
+                      float *dlogits, uint32_t N, uint32_t C) {
+  if constexpr (V <= kStepMaxV) {
+    if (want != V) {
+      ce_step_launch_v<V * 2>(want, grid, part, logits, labels, dloss, stats, loss, dlogits, N, C);
+      return;
+    }
+    const size_t lds = size_t(kStepBlock) * V * sizeof(f4);
+    ce_step_kernel<V><<<grid, kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss,
+                                                          dlogits, part, N, C,
+                                                          uint32_t(simd_end(N)));
+  }
+}
+
+// The one-pass step's arguments: -1 (after reporting) when unusable, 0 when the rows need the three
+// passes, else the float4 units per lane of the register-resident row (its LDS opt-in granted).
+int ce_step_form(const float *logits, const int32_t *labels, const float *dloss, const float *stats,
+                 const float *loss, const float *dlogits, uint64_t N, uint64_t C,
+                 const char *where) {
+  if (!logits || !labels || !dloss || !stats || !loss || !dlogits) {
+    report_error(where, "logits, labels, dloss, stats, loss and dlogits are required");
+    return -1;
+  }
+  if (C == 0 || C >= (uint64_t(1) << 31)) {
+    report_error(where, "rows of %llu elements are not supported", (unsigned long long)C);
+    return -1;
+  }
+  if (N >= (uint64_t(1) << 31)) {
+    report_error(where, "more than 2^31 rows are not supported (%llu)", (unsigned long long)N);
+    return -1;
+  }
+  // the column sums live in LDS (one float4 slot per lane and unit, the row's plus padding): the
+  // kernel must be allowed that much of it
+  if (C % 4 == 0 && C <= kStepMaxC && aligned16(logits) && aligned16(dlogits))
+    return ce_step_units<1>(C);
+  return 0;
+}
+
+// The one-pass step over `grid` workgroups with their column sums in part[grid][C], then their sum
+// into dbias when it is wanted.
+void ce_step_launch(int V, unsigned grid, float *part, const float *logits, const int32_t *labels,
+                    const float *dloss, float *stats, float *loss, float *dlogits, float *dbias,
+                    uint64_t N, uint64_t C) {
+  const uint32_t c32 = uint32_t(C);
+  ce_step_launch_v<1>(V, grid, part, logits, labels, dloss, stats, loss, dlogits, uint32_t(N), c32);
+  if (dbias) ce_step_finalize<<<ceil_div(C, kCeBlock), kCeBlock, 0, stream()>>>(part, dbias, c32, grid);
 }
 
 bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
@@ -1024,29 +1117,9 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   const char *where = "softmax_cross_entropy_step_hip";
   if (!ensure_init()) return;
   if (N == 0) return;
-  if (!logits || !labels || !dloss || !stats || !loss || !dlogits) {
-    report_error(where, "logits, labels, dloss, stats, loss and dlogits are required");
-    return;
-  }
-  if (C == 0 || C >= (uint64_t(1) << 31)) {
-    report_error(where, "rows of %llu elements are not supported", (unsigned long long)C);
-    return;
-  }
-  if (N >= (uint64_t(1) << 31)) {
-    report_error(where, "more than 2^31 rows are not supported (%llu)", (unsigned long long)N);
-    return;
-  }
-  const uint32_t c32 = uint32_t(C);
-  // float4 units per lane for a register-resident row (0: not this kernel)
-  int V = 0;
-  if (C % 4 == 0 && aligned16(logits) && aligned16(dlogits))
-    for (int v = 1; v <= 16 && !V; v *= 2)
-      if (C <= uint64_t(kStepBlock) * 4 * v) V = v;
-  // the column sums live in LDS (one float4 slot per lane and unit, the row's plus padding): the
-  // kernel must be allowed that much of it
-  const size_t lds = size_t(kStepBlock) * size_t(V) * sizeof(f4);
-  if (V && !ce_step_lds_ok(V, lds)) V = 0;
-  if (!V) {
+  const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
+  if (V < 0) return;
+  if (V == 0) {
     // any other row: the forward, the overwriting backward and the column sum as three passes
     Tensor tx, tl, ts, to, tg, tdx;
     memset(&tx, 0, sizeof tx);
@@ -1079,16 +1152,7 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   // the workgroups' column sums (written even when no bias gradient is wanted; then unread)
   float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
   if (!part) return;
-  const uint64_t se = simd_end(N);
-  switch (V) {
-  case 1: ce_step_kernel<1><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
-  case 2: ce_step_kernel<2><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
-  case 4: ce_step_kernel<4><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
-  case 8: ce_step_kernel<8><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
-  default: ce_step_kernel<16><<<unsigned(grid), kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss, dlogits, part, uint32_t(N), c32, uint32_t(se)); break;
-  }
-  if (dbias)
-    ce_step_finalize<<<ceil_div(C, kCeBlock), kCeBlock, 0, stream()>>>(part, dbias, c32, unsigned(grid));
+  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
   finish(where);
 }
 
