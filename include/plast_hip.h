@@ -200,6 +200,20 @@ void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, cons
                                     float *stats, float *loss, float *dlogits, float *dbias, u64 N,
                                     u64 C);
 
+/* softmax_cross_entropy_step_hip without allocating: same arguments and results, with its
+ * per-workgroup column sums in a fixed 32 MiB device array of the library (each GPU holds its own
+ * until the process ends) rather than in workspace. It calls no hipMalloc or other allocating
+ * routine, so it serves callers that cannot allocate: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation. Only one-pass rows are taken: C a multiple of 4 up to
+ * 32768, logits and dlogits 16-byte aligned, N below 2^31; anything else is reported as an error
+ * (the three-pass form allocates). The results are bit-identical to
+ * softmax_cross_entropy_step_hip's (the same kernels over the same grid). Calls that overlap on
+ * one GPU (other streams, other threads) share the array and race. No counterpart in the
+ * reference. */
+void softmax_cross_entropy_step_noalloc_hip(const float *logits, const i32 *labels,
+                                            const float *dloss, float *stats, float *loss,
+                                            float *dlogits, float *dbias, u64 N, u64 C);
+
 /* ------------------------------------------------------------------ pack / host transfer ----- */
 
 /* A contiguous image of a possibly strided tensor, layout-identical to CudaTensorPack

@@ -214,6 +214,8 @@ void report_error(const char *where, const char *fmt, ...) __attribute__((format
 hipStream_t stream();
 // Compute units of the library's device.
 int num_cus();
+// The device the library runs on (its stream's), fixed at initialisation.
+int library_device();
 // Called at the end of every entry point: checks the launch and, in synchronous mode, waits.
 void finish(const char *where);
 bool ensure_init();

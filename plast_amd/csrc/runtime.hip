@@ -55,6 +55,8 @@ hipStream_t stream() {
 
 int num_cus() { return g_cus > 0 ? g_cus : 1; }
 
+int library_device() { return g_device; }
+
 void finish(const char *where) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -11,12 +11,50 @@
 // stats[row] = (m, l) for the backward.
 // Backward: dx[row, j] (+)= dloss[row] * (exp((x - m) - l) - onehot).
 // The fast paths evaluate exp with exp_le0 (about 1 ulp); the exact-refold paths use expf.
+#include <atomic>
 #include <cfloat>
 
 #include "common.hpp"
 
+// Device scratch of the allocation-free one-pass step (softmax_cross_entropy_step_noalloc_hip):
+// the workgroups' column sums, kScratchFloats floats (32 MiB: 256 workgroups of rows up to 32768
+// floats, the widest one-pass row of 1024-lane workgroups; wider ones, of a build with narrower
+// workgroups, run on fewer workgroups). Each GPU the library runs on holds its own copy until the
+// process ends. Host code never passes this name to a kernel (it
+// is a host-side stand-in there): noalloc_scratch() looks the device address up once per device.
+static __device__ __align__(256) float scratch[uint64_t(1) << 23];
+
 namespace plast {
 namespace {
+
+constexpr uint64_t kScratchFloats = uint64_t(1) << 23;
+static_assert(sizeof(scratch) == kScratchFloats * sizeof(float), "scratch size");
+
+// The device address of `scratch` on the library's device, found with hipGetSymbolAddress, with
+// that device current, on the first call there (null, after reporting, when the lookup fails).
+float *noalloc_scratch(const char *where) {
+  static std::atomic<float *> addr[64] = {};
+  const int dev = library_device();
+  if (dev < 0 || dev >= 64) {
+    report_error(where, "device %d is out of range", dev);
+    return nullptr;
+  }
+  float *a = addr[dev].load(std::memory_order_acquire);
+  if (a) return a;
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  void *p = nullptr;
+  if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (cur >= 0 && cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess || !p) {
+    report_error(where, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    return nullptr;
+  }
+  a = static_cast<float *>(p);
+  addr[dev].store(a, std::memory_order_release);
+  return a;
+}
 
 constexpr int kCeBlock = 256;
 constexpr int kCeWaves = kCeBlock / 64;
@@ -1152,6 +1190,30 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   // the workgroups' column sums (written even when no bias gradient is wanted; then unread)
   float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
   if (!part) return;
+  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
+  finish(where);
+}
+
+void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *labels,
+                                            const float *dloss, float *stats, float *loss,
+                                            float *dlogits, float *dbias, u64 N, u64 C) {
+  const char *where = "softmax_cross_entropy_step_noalloc_hip";
+  if (!ensure_init()) return;
+  if (N == 0) return;
+  const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
+  if (V < 0) return;
+  if (V == 0) {
+    report_error(where, "rows of %llu floats are not one-pass rows (whole float4, 16-byte aligned "
+                 "logits and dlogits, at most %llu floats): the three-pass form allocates",
+                 (unsigned long long)C, (unsigned long long)kStepMaxC);
+    return;
+  }
+  float *part = noalloc_scratch(where);
+  if (!part) return;
+  // the grid the scratch holds (every workgroup of a CU-sized grid, up to 32768 floats a row)
+  uint64_t grid = N < uint64_t(num_cus()) * PLAST_CE_STEP_WPC ? N
+                                                               : uint64_t(num_cus()) * PLAST_CE_STEP_WPC;
+  if (grid > kScratchFloats / C) grid = kScratchFloats / C;
   ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
   finish(where);
 }

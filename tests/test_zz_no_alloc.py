@@ -1,0 +1,76 @@
+"""The allocation-free cross-entropy step (softmax_cross_entropy_step_noalloc_hip) against the
+allocating one (softmax_cross_entropy_step_hip) through the C-ABI: stats, loss, dlogits and the
+bias gradient bit for bit (both run the same kernels over the same grid for rows up to 32768
+floats), on calls in a row whose second input is smaller than the first (the device array keeps the
+previous call's contents), and the rejection of rows the one-pass kernel cannot take."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cases import assert_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rt, N, Cn, seed, special=False):
+    rng = np.random.RandomState(seed)
+    x = (rng.randn(N, Cn) * 2).astype(np.float32)
+    if special and N >= 4:
+        x[1, 3] = np.nan
+        x[2, :] = -np.inf
+        x[3, :] = -3.0e38
+        x[3, 0] = 3.0e38
+    lab = rng.randint(0, Cn, N).astype(np.int32)
+    g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)
+    return (rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab),
+            rt.DeviceTensor.from_numpy(g))
+
+
+def _run(rt, entry, X, Lb, G, with_bias=True):
+    N, Cn = X.shape
+    st = rt.DeviceTensor((N, 2), zero=False).fill_("uniform", 1, 5.0, 6.0)
+    loss = rt.DeviceTensor((N,), zero=False).fill_("uniform", 2, 5.0, 6.0)
+    dx = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 3, 5.0, 6.0)
+    db = rt.DeviceTensor((Cn,), zero=False).fill_("uniform", 4, 5.0, 6.0) if with_bias else None
+    L = rt.lib()
+    getattr(L, entry)(X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr,
+                      db.ptr if db is not None else None, N, Cn)
+    L.check(entry)
+    return [st.numpy(), loss.numpy(), dx.numpy()] + ([db.numpy()] if with_bias else [])
+
+
+def _same(rt, N, Cn, seed, special=False, with_bias=True):
+    print(f"no-alloc step {N}x{Cn} special={special} bias={with_bias}", flush=True)
+    X, Lb, G = _inputs(rt, N, Cn, seed, special)
+    got = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
+    want = _run(rt, "softmax_cross_entropy_step_hip", X, Lb, G, with_bias)
+    for name, a, b in zip(("stats", "loss", "dlogits", "dbias"), got, want):
+        assert_bits(a, b, f"{N}x{Cn} {name}")
+
+
+def test_two_calls_second_smaller():
+    from plast_amd import runtime as rt
+    _same(rt, 3000, 8192, 1)          # 256 workgroups of column sums in the device array
+    _same(rt, 37, 2048, 2)            # fewer workgroups and shorter rows: stale sums unread
+
+
+@pytest.mark.parametrize("N, Cn, special, with_bias", [
+    (13, 4, False, True), (64, 32000, True, True), (300, 32768, False, True),
+    (9, 32768, True, True), (40, 12000, False, False), (1, 1024, True, True)])
+def test_matches_allocating_step(N, Cn, special, with_bias):
+    from plast_amd import runtime as rt
+    _same(rt, N, Cn, N + Cn, special, with_bias)
+
+
+def test_rows_beyond_the_one_pass_kernel_are_rejected():
+    from plast_amd import runtime as rt
+    L = rt.lib()
+    for N, Cn in ((8, 6), (4, 32772), (3, 65536)):
+        X, Lb, G = _inputs(rt, N, Cn, 5)
+        st, loss = rt.DeviceTensor((N, 2)), rt.DeviceTensor((N,))
+        dx = rt.DeviceTensor((N, Cn))
+        L.softmax_cross_entropy_step_noalloc_hip(X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr,
+                                                 None, N, Cn)
+        with pytest.raises(rt.PlastHipError, match="not one-pass rows"):
+            L.check("noalloc")
