@@ -314,12 +314,23 @@ int plast_hip_synchronize(void);
  * frees it. Only device work can be captured: run each op once before capturing so that the
  * library's workspaces are already sized (a capture that would grow one fails with an error), and
  * keep host transfers and allocation outside. The library records fills as kernels, never as
- * memset nodes. Returns 0 / a non-null graph on success. No counterpart in the reference, which
- * launches and synchronises op by op. */
+ * memset nodes. A workspace that eager work outgrows while a graph is alive is kept (retired)
+ * until the last graph the library made is destroyed, so a replay never reaches freed memory.
+ * Returns 0 / a non-null graph on success. No counterpart in the reference, which launches and
+ * synchronises op by op. */
 int plast_hip_capture_begin(void);
 void *plast_hip_capture_end(void);
 int plast_hip_graph_launch(void *graph);
 void plast_hip_graph_destroy(void *graph);
+/* Grow workspace slot 0, 1 or 2 to at least `bytes` now (for instance before a capture; slot 0
+ * holds reduction and cross-entropy partial sums, 1 max/min backward tie counts, 2 pack staging),
+ * and the bytes a slot holds. Returns 0 on success. */
+int plast_hip_workspace_reserve(int slot, u64 bytes);
+u64 plast_hip_workspace_bytes(int slot);
+/* The graphs made by plast_hip_capture_end() and not yet destroyed, and the workspace buffers
+ * retired while they live (freed with the last of them). */
+int plast_hip_graphs_alive(void);
+int plast_hip_workspace_retired(void);
 /* The library's stream (a hipStream_t), for callers that order their own work against it. */
 void *plast_hip_stream(void);
 /* Number of errors since the last plast_hip_clear_error(), and the most recent message. */

@@ -4,6 +4,7 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "ws_ledger.hpp"
 
 namespace plast {
 
@@ -16,8 +17,7 @@ hipStream_t g_stream = nullptr;
 int g_err_count = 0;
 char g_err_msg[512] = "";
 constexpr int kSlots = 3;
-void *g_ws[kSlots] = {};
-size_t g_ws_bytes[kSlots] = {};
+WorkspaceLedger<kSlots> g_ws;  // workspace slots, and the graphs captured over them
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
 int g_cus = 256;  // compute units of the device (MI355X: 256), read at init
 }  // namespace
@@ -69,30 +69,34 @@ void finish(const char *where) {
   }
 }
 
+// Frees an outgrown workspace buffer once the work queued on the library stream (which may still
+// read it) has finished.
+static void release_workspace(void *p) {
+  (void)hipStreamSynchronize(g_stream);
+  (void)hipFree(p);
+}
+
 void *workspace(size_t bytes, int slot) {
   if (slot < 0 || slot >= kSlots) return nullptr;
-  if (bytes <= g_ws_bytes[slot]) return g_ws[slot];
+  if (bytes <= g_ws.bytes(slot)) return g_ws.buffer(slot);
   if (g_capturing) {
     report_error("workspace", "%zu bytes needed while capturing a graph: run the work once before "
                  "capturing it", bytes);
     return nullptr;
   }
-  // Work already queued may still read the old buffer.
-  if (g_ws[slot]) {
-    (void)hipStreamSynchronize(g_stream);
-    (void)hipFree(g_ws[slot]);
-    g_ws[slot] = nullptr;
-    g_ws_bytes[slot] = 0;
-  }
-  size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-  hipError_t e = hipMalloc(&g_ws[slot], want);
-  if (e != hipSuccess) {
-    report_error("workspace", "hipMalloc(%zu): %s", want, hipGetErrorString(e));
-    g_ws[slot] = nullptr;
-    return nullptr;
-  }
-  g_ws_bytes[slot] = want;
-  return g_ws[slot];
+  const size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+  return g_ws.grow(
+      slot, bytes, want,
+      [](size_t n) -> void * {
+        void *p = nullptr;
+        const hipError_t e = hipMalloc(&p, n);
+        if (e != hipSuccess) {
+          report_error("workspace", "hipMalloc(%zu): %s", n, hipGetErrorString(e));
+          return nullptr;
+        }
+        return p;
+      },
+      release_workspace);
 }
 
 // ------------------------------------------------------------------------- metadata helpers
@@ -336,6 +340,7 @@ void *plast_hip_capture_end(void) {
     report_error("plast_hip_capture_end", "instantiate: %s", hipGetErrorString(e));
     return nullptr;
   }
+  g_ws.graph_created(exec);
   return exec;
 }
 
@@ -356,8 +361,30 @@ int plast_hip_graph_launch(void *graph) {
 }
 
 void plast_hip_graph_destroy(void *graph) {
-  if (graph) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+  if (!graph) return;
+  // a replay may still be running on the library stream
+  if (g_inited) (void)hipStreamSynchronize(g_stream);
+  (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+  // the last graph gone: free the workspace buffers that were outgrown while graphs held them
+  g_ws.graph_destroyed(graph, release_workspace);
 }
+
+int plast_hip_workspace_reserve(int slot, uint64_t bytes) {
+  if (!ensure_init()) return -1;
+  if (slot < 0 || slot >= kSlots) {
+    report_error("plast_hip_workspace_reserve", "slot %d is not one of 0..%d", slot, kSlots - 1);
+    return -1;
+  }
+  return bytes == 0 || workspace(size_t(bytes), slot) ? 0 : -1;
+}
+
+uint64_t plast_hip_workspace_bytes(int slot) {
+  return slot >= 0 && slot < kSlots ? uint64_t(g_ws.bytes(slot)) : 0;
+}
+
+int plast_hip_graphs_alive(void) { return int(g_ws.live_graphs()); }
+
+int plast_hip_workspace_retired(void) { return int(g_ws.retired()); }
 
 int plast_hip_synchronize(void) {
   if (!ensure_init()) return -1;

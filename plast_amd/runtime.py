@@ -52,6 +52,10 @@ class Library:
             "plast_hip_capture_end": ([], C.c_void_p),
             "plast_hip_graph_launch": ([C.c_void_p], C.c_int),
             "plast_hip_graph_destroy": ([C.c_void_p], None),
+            "plast_hip_workspace_reserve": ([C.c_int, C.c_uint64], C.c_int),
+            "plast_hip_workspace_bytes": ([C.c_int], C.c_uint64),
+            "plast_hip_graphs_alive": ([], C.c_int),
+            "plast_hip_workspace_retired": ([], C.c_int),
             "plast_hip_stream": ([], C.c_void_p),
             "plast_hip_error_count": ([], C.c_int),
             "plast_hip_last_error": ([], C.c_char_p),

@@ -171,3 +171,68 @@ def test_capture_errors():
     assert L.plast_hip_capture_end() is None                   # nothing open
     assert L.plast_hip_error_count() == 1
     L.plast_hip_clear_error()
+
+
+def test_workspace_outgrown_while_a_graph_lives():
+    """Config 1's step (its grad_b partial sums in workspace slot 0) captured; then eager work grows
+    slot 0 (a reserve past its size, then a cross-entropy step whose partial sums need more): the
+    outgrown buffers are retired, not freed, so every replay still reads and writes the buffer it
+    was recorded with and matches the eager step bit for bit; destroying the graph frees them."""
+    from plast_amd import abi, ops
+    from plast_amd.abi import KernelParams
+    rt = _rt()
+    L = rt.lib()
+    print("graph: workspace outgrown while the graph lives", flush=True)
+    X, b, gy = (rt.DeviceTensor(s, zero=False) for s in ((1024, 256), (256,), (1024, 256)))
+    Y, gb = rt.DeviceTensor((1024, 256), zero=False), rt.DeviceTensor((256,), zero=False)
+    tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
+                          ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
+
+    def step():
+        rt.forward("fused_elementwise", [X, b], Y, KernelParams(C.addressof(tape), 0, 0.0))
+        rt.forward("sum", [gy], gb, KernelParams(0, 0, 0.0))
+
+    rng = np.random.RandomState(3)
+
+    def fresh():
+        for t, shape in ((X, (1024, 256)), (b, (256,)), (gy, (1024, 256))):
+            _h2d(t, rng.uniform(-1, 1, shape))
+
+    fresh()
+    step()
+    alive0, retired0 = L.plast_hip_graphs_alive(), L.plast_hip_workspace_retired()
+    assert L.plast_hip_capture_begin() == 0
+    step()
+    graph = L.plast_hip_capture_end()
+    L.check("capture")
+    assert graph and L.plast_hip_graphs_alive() == alive0 + 1
+    try:
+        size0 = L.plast_hip_workspace_bytes(0)
+        assert L.plast_hip_workspace_reserve(0, size0 + (1 << 20)) == 0
+        L.check("reserve")
+        assert L.plast_hip_workspace_bytes(0) >= size0 + (1 << 20)
+        assert L.plast_hip_workspace_retired() == retired0 + 1
+        # a cross-entropy step whose 256 workgroups' column sums outgrow slot 0 again
+        N, Cn = 512, 4 * (L.plast_hip_workspace_bytes(0) // (256 * 4 * 4) + 1)
+        logits = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 7, -2.0, 2.0)
+        labels = rt.DeviceTensor.from_numpy(rng.randint(0, Cn, N).astype(np.int32))
+        dloss = rt.DeviceTensor.from_numpy(np.full(N, 1.0 / N, np.float32))
+        st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
+        dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
+        if Cn <= 32768:
+            L.softmax_cross_entropy_step_hip(logits.ptr, labels.ptr, dloss.ptr, st.ptr, loss.ptr,
+                                             dx.ptr, db.ptr, N, Cn)
+            L.check("ce step")
+            assert L.plast_hip_workspace_retired() == retired0 + 2
+        for rep in range(3):
+            fresh()
+            assert L.plast_hip_graph_launch(graph) == 0
+            y_g, gb_g = Y.numpy(), gb.numpy()
+            step()                           # eagerly, through the grown slot
+            assert_bits(y_g, Y.numpy(), f"replay {rep}: relu(X + b)")
+            assert_bits(gb_g, gb.numpy(), f"replay {rep}: grad_b")
+    finally:
+        L.plast_hip_graph_destroy(graph)
+    assert L.plast_hip_graphs_alive() == alive0
+    if alive0 == 0:
+        assert L.plast_hip_workspace_retired() == 0
