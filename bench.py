@@ -168,8 +168,8 @@ class C2Fused(Workload):
 
 class C1(Workload):
     """Config 1: Y = relu(X + b), X [1024,256], b [256] ~ U(-1,1); grad_b = sum_0 grad_Y. "big":
-    the same fused chain over [16384, 4096] (a layer of realistic width, through the compiled
-    rows form)."""
+    the same fused chain over [16384, 4096] (a layer of realistic width, through the tape
+    interpreter's rows form)."""
 
     def __init__(self, part):
         self.part = part
@@ -220,6 +220,26 @@ class C1(Workload):
         else:
             if lib().plast_hip_graph_launch(self.graph) != 0:
                 raise SystemExit("bench.py: graph launch failed")
+
+    def kernel_us(self, calls: int = 100, reps: int = 5):
+        """Device microseconds per call without the host's per-call cost: `calls` back-to-back
+        calls captured as one graph, replayed `reps` times (the graph launch is spread over the
+        calls). None for the graph workload itself."""
+        if self.part not in ("fwd", "bwd"):
+            return None
+        L = lib()
+        self.step()  # sizes the workspaces outside the capture
+        if L.plast_hip_capture_begin() != 0:
+            raise SystemExit("bench.py: graph capture failed")
+        for _ in range(calls):
+            self.step()
+        g = L.plast_hip_capture_end()
+        L.check("capture")
+        try:
+            ms = timed(lambda: L.plast_hip_graph_launch(g), reps, 2)
+        finally:
+            L.plast_hip_graph_destroy(g)
+        return round(ms * 1e3 / calls, 2)
 
     def free(self):
         if self.graph:
@@ -658,6 +678,12 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     gbs = w.bytes_per_call / (ms * 1e-3) / 1e9
     r = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
          "elems_per_s": round(w.elems / (ms * 1e-3), 1), "algorithmic_bytes": w.bytes_per_call}
+    if isinstance(w, C1) and w.part != "big":
+        # latency-bound: microseconds per call as the caller sees them, and on the device alone
+        r["us_per_call"] = round(ms * 1e3, 2)
+        k = w.kernel_us()
+        if k is not None:
+            r["kernel_us_per_call"] = k
     return r
 
 

@@ -50,25 +50,6 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_TAPE_XCD
 #define PLAST_TAPE_XCD 0
 #endif
-// Flat fused chains (every input unit-stride or one broadcast scalar) run the streaming form of the
-// interpreter: SWPC workgroups of SBLOCK lanes per CU, each walking a contiguous range of float4
-// units SUNROLL per lane at a time, with the next step's operands loaded before the current step is
-// interpreted. STREAM 0 sends them to the one-shot vector kernel instead.
-#ifndef PLAST_TAPE_STREAM
-#define PLAST_TAPE_STREAM 0
-#endif
-#ifndef PLAST_TAPE_SBLOCK
-#define PLAST_TAPE_SBLOCK 256
-#endif
-#ifndef PLAST_TAPE_SWPC
-#define PLAST_TAPE_SWPC 8
-#endif
-#ifndef PLAST_TAPE_SUNROLL
-#define PLAST_TAPE_SUNROLL 1
-#endif
-#ifndef PLAST_TAPE_SMODE
-#define PLAST_TAPE_SMODE 0  // 0: grid-stride steps, 1: a contiguous range of steps per workgroup
-#endif
 #ifndef PLAST_TAPE_TILE_ROWS
 #define PLAST_TAPE_TILE_ROWS 2  // fused chains in the transposed-operand tile: rows per evaluation
 #endif
@@ -100,6 +81,14 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // +3%, the [16384, 4096] bias gradient unchanged; 4 lanes lost 5% on that bias gradient.
 #ifndef PLAST_COL_FIN_Q
 #define PLAST_COL_FIN_Q 8
+#endif
+// Small leading-axis sums (at most PLAST_COL_SMALL_MAX input elements) in one launch: workgroups
+// of PLAST_COL_SMALL_S4 float4 columns that walk every row, instead of row chunks plus a finalize.
+#ifndef PLAST_COL_SMALL_MAX
+#define PLAST_COL_SMALL_MAX (1u << 21)
+#endif
+#ifndef PLAST_COL_SMALL_S4
+#define PLAST_COL_SMALL_S4 4
 #endif
 #ifndef PLAST_COL_BLOCKS
 #define PLAST_COL_BLOCKS 1024  // workgroups a leading-axis reduction is chunked up to
@@ -162,6 +151,21 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 #ifndef PLAST_CE_BWD_MODE
 #define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
+#endif
+// Softmax forward over rows of 2048..32768 floats: 1 = persistent 1024-lane workgroups (one per
+// CU) walking rows with the next row's loads in flight; 0 = one 256-lane workgroup per row.
+// Measured at [32768, 32000]: 5.86-5.89 TB/s against 5.33-5.39.
+#ifndef PLAST_SOFTMAX_FWD_STEP
+#define PLAST_SOFTMAX_FWD_STEP 1
+#endif
+// Softmax forward and backward variants measured at [32768, 32000] in one process (so on the same
+// box and in the same process state): the persistent forward with one barrier per row (per-wave
+// maxima and sums merged after it) 5.81 TB/s against 5.89 for two; the backward with the input
+// gradient's loads issued with y and dy 5.64 against 5.62-5.64 without, and 5.54-5.65 at 1024
+// lanes. Neither was kept.
+// Softmax backward, rows held in registers: lanes per row.
+#ifndef PLAST_SOFTMAX_BWD_BLOCK
+#define PLAST_SOFTMAX_BWD_BLOCK 512
 #endif
 #ifndef PLAST_SOFTMAX_BLOCK
 #define PLAST_SOFTMAX_BLOCK 256  // softmax rows held in registers: lanes per row

@@ -117,107 +117,6 @@ __global__ __launch_bounds__((VecLaunch<Body, REUSE>::block)) void ew_vec_kernel
     if (valid[u]) store_stream<kNtStore>(r[u], reinterpret_cast<f4 *>(A.out + oo[u]));
 }
 
-// Streaming form of a flat fused chain (Body a TapeBody): every input is unit-stride or one
-// broadcast scalar (bit k of A.bcast_inner). The grid is a fixed number of workgroups that walk the
-// space in steps of SUNROLL * SBLOCK float4 units, and each workgroup loads its next step's
-// operands before interpreting the current one, so the interpreter's scalar dispatch overlaps the
-// memory latency instead of adding to it. Each wave reads and writes whole 1 KiB runs per operand
-// per unit. SMODE 0: workgroup b takes the steps b, b + G, b + 2G, ... (the grid advances over one
-// contiguous front); 1: workgroup b (XCD-contiguous numbering) takes a contiguous range of steps.
-template <class Body>
-__global__ __launch_bounds__(PLAST_TAPE_SBLOCK) void ew_tape_stream_kernel(EwArgs<Body::NIN> A,
-                                                                           Body body,
-                                                                           uint64_t per_block) {
-  constexpr int NIN = Body::NIN;
-  constexpr int B = PLAST_TAPE_SBLOCK, U = PLAST_TAPE_SUNROLL;
-  constexpr uint64_t S = uint64_t(B) * U;
-  // step indices are 32-bit (the host checks the count): a 64-bit bound compare would be made in
-  // vector registers, which the loop head may find still tied to an in-flight memory operation
-  const uint32_t nsteps = uint32_t((A.units + S - 1) / S);
-  uint32_t first, stride, last;
-  if (PLAST_TAPE_SMODE == 0) {
-    first = blockIdx.x, stride = gridDim.x, last = nsteps;
-  } else {
-    const uint32_t per = uint32_t(per_block / S);
-    first = xcd_block(blockIdx.x, gridDim.x) * per, stride = 1;
-    last = first + per < nsteps ? first + per : nsteps;
-  }
-  if (first >= last) return;
-  const uint64_t end = A.units;
-  // broadcast scalars: loaded once
-  f4 bc[NIN];
-#pragma unroll
-  for (int k = 0; k < NIN; ++k) bc[k] = (A.bcast_inner >> k & 1u) ? f4(A.in[k][0]) : f4(0.0f);
-  // Loads are issued unconditionally (a unit past the end re-reads the last unit; the step past the
-  // last is the last one again): a load under a branch may not have been issued, so the wait before
-  // a step's first use could not count the prefetch as outstanding and would wait for it too.
-  auto load = [&](uint32_t j, f4 (&x)[U][NIN]) {
-    if (j >= last) j = last - 1;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      uint64_t q = uint64_t(j) * S + uint64_t(u) * B + threadIdx.x;
-      if (q >= end) q = end - 1;
-#pragma unroll
-      for (int k = 0; k < NIN; ++k) {
-        if (A.bcast_inner >> k & 1u) x[u][k] = bc[k];
-        else x[u][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A.in[k]) + q);
-      }
-    }
-  };
-  const uint32_t words = body.load_words();
-  // one step: interpret the units of step j held in x, store them
-  auto step = [&](uint32_t j, const f4 (&x)[U][NIN]) {
-    // every operand consumed here on every path (see ce_step_kernel: a load left pending past the
-    // back edge makes the loop head wait for all loads)
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int k = 0; k < NIN; ++k)
-        asm volatile("" ::"v"(x[u][k][0]), "v"(x[u][k][1]), "v"(x[u][k][2]), "v"(x[u][k][3]));
-    uint64_t idx[U];
-    bool valid[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint64_t q = uint64_t(j) * S + uint64_t(u) * B + threadIdx.x;
-      idx[u] = q * 4;
-      valid[u] = q < end;
-    }
-    f4 r[U];
-    body.template eval_units_with<U>(words, x, idx, valid, r);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (valid[u]) reinterpret_cast<f4 *>(A.out)[idx[u] / 4] = r[u];
-  };
-  // Two register sets used in turn, so a step's operands are never copied: a copy out of a
-  // set whose loads are still in flight would wait for them and serialise memory and interpretation.
-  // Each set is reloaded right after its step is interpreted, so the youngest memory operations at
-  // the loop's back edge are loads (a wait there for a store's registers leaves them in flight).
-  f4 xa[U][NIN], xb[U][NIN];
-  load(first, xa);
-  load(first + stride, xb);
-  for (uint32_t j = first; j < last; j += 2 * stride) {
-    step(j, xa);
-    load(j + 2 * stride, xa);
-    if (j + stride >= last) break;
-    step(j + stride, xb);
-    load(j + 3 * stride, xb);
-  }
-}
-
-// Launch the streaming form over A.units float4 units (flat space, A filled by the vector path).
-template <class Body>
-bool launch_tape_stream(const EwArgs<Body::NIN> &A, const Body &body) {
-  constexpr uint64_t step = uint64_t(PLAST_TAPE_SBLOCK) * PLAST_TAPE_SUNROLL;
-  const uint64_t steps = (A.units + step - 1) / step;
-  if (steps >= (uint64_t(1) << 31)) return false;
-  uint64_t grid = uint64_t(num_cus()) * PLAST_TAPE_SWPC;
-  if (grid > steps) grid = steps;
-  const uint64_t per_block = (steps + grid - 1) / grid * step;
-  if (PLAST_TAPE_SMODE != 0) grid = (A.units + per_block - 1) / per_block;
-  ew_tape_stream_kernel<Body><<<unsigned(grid), PLAST_TAPE_SBLOCK, 0, stream()>>>(A, body, per_block);
-  return true;
-}
-
 // Generic kernel: any strides, one element per lane per step. IDX64 selects 64-bit division for
 // spaces of 2^32 elements or more. The loop runs per workgroup, not per lane, so every lane is
 // active when the body is evaluated (the tape interpreter reads its instruction words across the
@@ -712,11 +611,6 @@ bool launch_elementwise(const Body &body, const void *const *in, void *out, Spac
     A.units = n / 4;
     A.dinner4 = MagicDiv::make(uint32_t(inner / 4));
     for (int d = 0; d < in_ax; ++d) A.dv[d] = MagicDiv::make(uint32_t(s.shape[d]));
-    if constexpr (Body::kTape) {
-      if (PLAST_TAPE_STREAM && in_ax == 0 && (A.reused & ~A.bcast_inner) == 0 &&
-          launch_tape_stream(A, body))
-        return true;
-    }
     // a broadcast-inner operand is a scalar load; only float4-streamed operands decide the policy
     const bool done = (A.reused & ~A.bcast_inner) != 0 ? launch_vec<Body, true>(A, body, in_ax)
                                                        : launch_vec<Body, false>(A, body, in_ax);

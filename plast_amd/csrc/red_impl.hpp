@@ -643,6 +643,82 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   }
 }
 
+// Small leading-axis sums in one launch (no partials leave the workgroup, so no finalize), also
+// for a storing producer (the one-pass epilogue), which then sums in the same order as the plain
+// sum of what it stores. A workgroup owns S4 float4 columns (4 * S4 adjacent outputs) of one outer index and walks every row
+// of the reduced axis: lane (g, c) sums the rows g, g + G, g + 2G, ... (G = kBlock / S4 row groups)
+// of float4 column c in order. The row groups of a wave then merge with a fixed butterfly, and the
+// four waves' partials in wave order: the result is deterministic. A column whose sum is not finite
+// is summed again serially in index order (the reference's order decides such sums).
+template <class Prod>
+__global__ __launch_bounds__(kBlock) void red_cols_small_kernel(RedArgs<Prod::NIN> A, Prod prod,
+                                                                uint32_t xblocks) {
+  constexpr int NIN = Prod::NIN;
+  constexpr int S4 = PLAST_COL_SMALL_S4, G = kBlock / S4, kU = 8;
+  static_assert(64 % S4 == 0, "row groups split evenly over the waves");
+  __shared__ f4 sh[kBlock / 64][S4];
+  const uint32_t t = threadIdx.x, c4 = t % S4, g = t / S4, lane = t & 63, wv = t >> 6;
+  const uint32_t o = blockIdx.x / xblocks;
+  const uint64_t j0 = uint64_t(blockIdx.x - o * xblocks) * (4 * S4);  // the slice's first column
+  const uint64_t j = j0 + 4 * c4;
+  const bool active = j < A.inner;
+  int64_t base0[NIN], base[NIN], tbase;
+  decode_outer(A, o, base0, tbase);
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) base[k] = base0[k] + int64_t(j) * A.kst[k];
+  f4 f = f4(0.0f);
+  for (uint64_t r0 = g; r0 < A.len; r0 += uint64_t(G) * kU) {
+    f4 xv[kU][NIN];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint64_t r = r0 + uint64_t(u) * G;
+      if (!active || r >= A.len) continue;
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) {
+        const float *src = A.in[k] + base[k] + int64_t(r) * A.rst[k];
+        xv[u][k] = (A.vec_mask >> k & 1u) ? *reinterpret_cast<const f4 *>(src) : f4(src[0]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint64_t r = r0 + uint64_t(u) * G;
+      if (!active || r >= A.len) continue;
+      f4 yv;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float v[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
+        yv[c] = prod.eval(v);
+        f[c] = f[c] + yv[c];
+      }
+      if constexpr (kStores<Prod>)  // a storing producer also writes each value it sums
+        *reinterpret_cast<f4 *>(prod.dst + base[0] + int64_t(r) * A.rst[0]) = yv;
+    }
+  }
+  // the wave's row groups (lanes c4, c4 + S4, ...) merge pairwise with a fixed butterfly
+#pragma unroll
+  for (int m = S4; m < 64; m <<= 1)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) f[c] = f[c] + __shfl_xor(f[c], m);
+  if (lane < uint32_t(S4)) sh[wv][lane] = f;
+  __syncthreads();
+  if (t >= uint32_t(4 * S4)) return;
+  // lane t finishes output column j0 + t: the waves' partials in wave order
+  const uint64_t jc = j0 + t;
+  if (jc >= A.inner) return;
+  float p = sh[0][t / 4][t % 4];
+#pragma unroll
+  for (int w = 1; w < kBlock / 64; ++w) p = p + sh[w][t / 4][t % 4];
+  if (!finite_sum(p)) {
+    int64_t bc[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) bc[k] = base0[k] + int64_t(jc) * A.kst[k];
+    p = serial_sum_lane(A, prod, bc, A.len);
+  }
+  store_final<SumComb>(A.out, tbase + int64_t(jc) * A.tkst, p, A.post, A.divisor);
+}
+
 template <class Prod, class Comb>
 __global__ __launch_bounds__(kBlock) void red_cols_finalize(RedArgs<Prod::NIN> A, Prod prod) {
   using Part = typename Comb::Part;
@@ -932,6 +1008,15 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
     A.seglen = seglen;
     A.post = int(post);
     A.divisor = divisor;
+    if constexpr (std::is_same<Comb, SumComb>::value) {
+      // small: one launch over narrow column slices instead of chunks plus a finalize
+      if (chunks > 1 && vec && A.len * nout <= PLAST_COL_SMALL_MAX) {
+        const uint32_t sblocks = ceil_div(A.inner, uint64_t(4) * PLAST_COL_SMALL_S4);
+        red_cols_small_kernel<Prod><<<unsigned(uint64_t(sblocks) * A.rows), kBlock, 0, stream()>>>(
+            A, prod, sblocks);
+        return true;
+      }
+    }
     if (base_blocks <= max_blocks(kBlock)) {
       if (chunks > 1) {
         A.part = workspace(sizeof(Part) * nout * chunks);

@@ -900,6 +900,148 @@ __global__ __launch_bounds__(BS) void softmax_fwd_reg_kernel(const float *__rest
   }
 }
 
+// Softmax / log-softmax forward over rows of whole float4 (up to kStepBlock * 4 * V floats) by
+// persistent kStepBlock-lane workgroups, one per CU, walking rows G apart with the next row's loads
+// in flight while the current one is reduced: the row loop of ce_step_kernel (two register sets,
+// unconditional clamped loads, every loaded value consumed on every path). Per row: the reference's
+// max (row_max_exact's rules: the fast maximum unless the row holds a NaN or its maximum is zero,
+// then the serial fold), then e = exp(x - max) and its sum in the block's fixed order, then
+// y = e * (1 / S) or (x - max) - log S. Without a NaN every x - max is <= 0 or -inf, where exp_le0
+// holds (about 1 ulp); a row with a NaN, whose fold may stop below some elements, takes expf and a
+// division.
+template <bool LOG, int V>
+__global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const float *__restrict__ x,
+                                                                      float *__restrict__ y,
+                                                                      uint32_t N, uint32_t C) {
+  constexpr int BS = kStepBlock, W = BS / 64;
+  // one area per reduction round (see ce_step_kernel)
+  __shared__ float red1[2 * W], red2[W], ex[2];
+  const uint32_t C4 = C / 4, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint32_t G = gridDim.x;
+  const float ninf = -__builtin_huge_valf();
+  auto lane_index = [&]() {
+    uint32_t i = t;
+    asm volatile("" : "+v"(i));
+    return i;
+  };
+  auto load_row = [&](uint32_t r, f4 (&v)[V]) {
+    const char *xr = reinterpret_cast<const char *>(x + uint64_t(r < N ? r : N - 1) * C);
+    const uint32_t ti = lane_index();
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+      const uint32_t q = ti + uint32_t(u) * BS;
+      const uint32_t off = (q < C4 ? q : C4 - 1) * 16u;
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + off));
+    }
+  };
+  auto process = [&](uint32_t r, f4 (&v)[V]) {
+#pragma unroll
+    for (int u = 0; u < V; ++u) asm volatile("" ::"v"(v[u][0]), "v"(v[u][1]), "v"(v[u][2]), "v"(v[u][3]));
+    const uint32_t ti = lane_index();
+    const uint32_t full = C4 / BS;
+    // round 1: the fast maximum and whether the row holds a NaN (lanes past the row hold a copy of
+    // its last float4, which changes neither)
+    float m = ninf;
+    bool nan = false;
+#pragma unroll
+    for (int u = 0; u < V; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        m = fmaxf(m, v[u][c]);
+        nan = nan || v[u][c] != v[u][c];
+      }
+    m = wave_max(m);
+    const float nanw = wave_max(nan ? 1.0f : 0.0f);
+    if (lane == 0) {
+      red1[wave] = m;
+      red1[W + wave] = nanw;
+    }
+    __syncthreads();
+    float M = red1[0], anynan = red1[W];
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      M = fmaxf(M, red1[w]);
+      anynan = fmaxf(anynan, red1[W + w]);
+    }
+    const bool special = anynan != 0.0f;
+    float mx;
+    if (special || M == 0.0f) {
+      if (t == 0) ex[0] = serial_max_fold(x + uint64_t(r) * C, C);
+      __syncthreads();
+      mx = ex[0];
+    } else {
+      mx = M > -FLT_MAX ? M : -FLT_MAX;
+    }
+    // round 2: e = exp(x - mx), kept in v (log-softmax keeps x - mx), and the row's sum. A row with
+    // a NaN is summed from memory with expf instead (rare; it keeps the registers of the fast
+    // path free), each lane over the same elements in the same order as the fast path.
+    const f4 *x4 = reinterpret_cast<const f4 *>(x + uint64_t(r) * C);
+    float sl = 0.0f;
+    if (!special) {
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const bool in = uint32_t(u) < full || ti + uint32_t(u) * BS < C4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float d = v[u][c] - mx;
+          const float e = exp_le0(d);
+          v[u][c] = LOG ? d : e;
+          sl += in ? e : 0.0f;
+        }
+      }
+    } else {
+      for (uint32_t q = ti; q < C4; q += BS) {
+        const f4 xv = x4[q];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sl += expf(xv[c] - mx);
+      }
+    }
+    sl = wave_sum(sl);
+    if (lane == 0) red2[wave] = sl;
+    __syncthreads();
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) S += red2[w];
+    f4 *y4 = reinterpret_cast<f4 *>(y + uint64_t(r) * C);
+    char *dr = reinterpret_cast<char *>(y4);
+    const float l = LOG ? logf(S) : 0.0f;
+    if (!special) {
+      const float inv = 1.0f / S;
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const uint32_t q = ti + uint32_t(u) * BS;
+        f4 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = LOG ? v[u][c] - l : v[u][c] * inv;
+        if (uint32_t(u) < full || q < C4)
+          store_stream<true>(o, reinterpret_cast<f4 *>(dr + q * 16u));
+      }
+    } else {
+      for (uint32_t q = ti; q < C4; q += BS) {
+        const f4 xv = x4[q];
+        f4 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float d = xv[c] - mx;
+          o[c] = LOG ? d - l : expf(d) / S;
+        }
+        y4[q] = o;
+      }
+    }
+  };
+  uint32_t r = blockIdx.x;
+  f4 xa[V], xb[V];
+  load_row(r, xa);
+  load_row(r + G, xb);
+  for (; r < N; r += 2 * G) {
+    process(r, xa);
+    load_row(r + 2 * G, xa);
+    if (r + G >= N) break;
+    process(r + G, xb);
+    load_row(r + 3 * G, xb);
+  }
+}
+
 // Backward from the forward output y: dx += y * (dy - sum_j dy_j y_j) (softmax) or
 // dx += dy - expf(y) * sum_j dy_j (log-softmax), the gradient of the reference chain (its MAX
 // branch contributes zero in exact arithmetic); the row sum in the block's fixed order.
@@ -934,18 +1076,24 @@ __global__ __launch_bounds__(BS) void softmax_bwd_reg_kernel(const float *__rest
   const f4 *y4 = reinterpret_cast<const f4 *>(y + row * C);
   const f4 *g4 = reinterpret_cast<const f4 *>(dy + row * C);
   f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
+  // Loads are unconditional (a lane past the row reads the row's last float4, masked where it is
+  // used): the compiler waits for every outstanding load before the first use of a lane-masked
+  // one.
   f4 yv[V], gv[V];
 #pragma unroll
   for (int u = 0; u < V; ++u) {
     const uint32_t q = threadIdx.x + uint32_t(u) * BS;
-    yv[u] = q < C4 ? __builtin_nontemporal_load(y4 + q) : f4(0.0f);
-    gv[u] = q < C4 ? __builtin_nontemporal_load(g4 + q) : f4(0.0f);
+    const uint32_t qc = q < C4 ? q : C4 - 1;
+    yv[u] = __builtin_nontemporal_load(y4 + qc);
+    gv[u] = __builtin_nontemporal_load(g4 + qc);
   }
   float t = 0.0f;
 #pragma unroll
-  for (int u = 0; u < V; ++u)
+  for (int u = 0; u < V; ++u) {
+    const bool in = threadIdx.x + uint32_t(u) * BS < C4;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) t += LOG ? gv[u][c] : gv[u][c] * yv[u][c];
+    for (int c = 0; c < 4; ++c) t += in ? (LOG ? gv[u][c] : gv[u][c] * yv[u][c]) : 0.0f;
+  }
   t = block_sum<W>(t, lds);
 #pragma unroll
   for (int u = 0; u < V; ++u) {
@@ -994,6 +1142,25 @@ void softmax_forward(const Tensor **inputs, Tensor *output, KernelParams params,
   if (C % 4 == 0 && aligned16(x->data) && aligned16(output->data))
     for (int v = 1; v <= 32 && !V; v *= 2)
       if (uint64_t(C) <= uint64_t(kSoftmaxBlock) * 4 * v) V = v;
+  // rows of 2048..32768 floats: the persistent form (rows at a time below 2^31)
+  int SV = 0;
+  if (PLAST_SOFTMAX_FWD_STEP && V && C >= 2048 && N < (uint64_t(1) << 31))
+    for (int v = 1; v <= 8 && !SV; v *= 2)
+      if (uint64_t(C) <= uint64_t(kStepBlock) * 4 * v) SV = v;
+  if (SV) {
+    const unsigned G = unsigned(N < uint64_t(num_cus()) ? N : uint64_t(num_cus()));
+    const float *px = static_cast<const float *>(x->data);
+    float *py = static_cast<float *>(output->data);
+    const uint32_t n32 = uint32_t(N);
+    switch (SV) {
+      case 1: softmax_fwd_step_kernel<LOG, 1><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      case 2: softmax_fwd_step_kernel<LOG, 2><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      case 4: softmax_fwd_step_kernel<LOG, 4><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      default: softmax_fwd_step_kernel<LOG, 8><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+    }
+    finish(where);
+    return;
+  }
   for (uint64_t r0 = 0; r0 < N; r0 += R) {
     const unsigned n = unsigned(N - r0 < R ? N - r0 : R);
     const float *px = static_cast<const float *>(x->data) + r0 * C;
@@ -1025,11 +1192,12 @@ void softmax_backward(Tensor **inputs, const Tensor *output, KernelParams params
   const uint32_t C = uint32_t(x->shape[x->ndim - 1]);
   const uint64_t N = C ? numel(x) / C : 0;
   const uint64_t R = max_blocks(kCeBlock);
-  constexpr int BS = 512;  // y and dy in registers: 512 lanes keep V at 16 for 32768-float rows
+  constexpr int BS = PLAST_SOFTMAX_BWD_BLOCK;  // y and dy in registers: 512 lanes keep V at 16
+                                              // for 32768-float rows
   int V = 0;
   if (C % 4 == 0 && aligned16(output->data) && aligned16(output->grad->data) &&
       aligned16(x->grad->data))
-    for (int v = 1; v <= 16 && !V; v *= 2)
+    for (int v = 1; v <= 16 && !V && v * BS <= 8192; v *= 2)
       if (uint64_t(C) <= uint64_t(BS) * 4 * v) V = v;
   for (uint64_t r0 = 0; r0 < N; r0 += R) {
     const unsigned n = unsigned(N - r0 < R ? N - r0 : R);
@@ -1041,7 +1209,10 @@ void softmax_backward(Tensor **inputs, const Tensor *output, KernelParams params
       case 2: softmax_bwd_reg_kernel<LOG, 2, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
       case 4: softmax_bwd_reg_kernel<LOG, 4, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
       case 8: softmax_bwd_reg_kernel<LOG, 8, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
-      case 16: softmax_bwd_reg_kernel<LOG, 16, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C); break;
+      case 16:
+        if constexpr (16 * BS <= 8192)
+          softmax_bwd_reg_kernel<LOG, 16, BS><<<n, BS, 0, stream()>>>(py, pg, pd, C);
+        break;
       default: softmax_bwd_kernel<LOG><<<n, kCeBlock, 0, stream()>>>(py, pg, pd, C); break;
     }
   }

@@ -6,8 +6,8 @@ counts as equal). The host's glibc version is printed with the result. Measured 
 glibc 2.35: worst case 1 ulp for exp, 2 ulp for log, sin, cos and tan.
 
 The same sweep runs through a one-instruction fused chain ([LOAD, op]) as well: the tape
-interpreter's streaming form instantiates the same ocml functions in another kernel, so this pins
-the fused chains' math to glibc too."""
+interpreter instantiates the same ocml functions in another kernel, so this pins the fused
+chains' math to glibc too."""
 from __future__ import annotations
 
 import concurrent.futures as cf

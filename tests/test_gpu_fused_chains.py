@@ -1,6 +1,6 @@
 """GPU parity of fused elementwise chains (the tape interpreter, the only fused path): every
 chain_cases.TAPES case over a flat space (2^20 + 4 elements, so the last float4 falls in the NEG
-rule's tail; this runs the streaming form), over whole and partial transposed-operand tiles and over
+rule's tail; this runs the one-shot vector kernel), over whole and partial transposed-operand tiles and over
 [rows, inner] layouts with a re-read bias row and per-row scalars. Each fused result must equal the
 unfused chain of library ops bit for bit, and, where the chain's error is bounded per element, the
 oracle's unfused chain (bit-exact arithmetic, 2 ulp for a final exp). Inputs hold ±0, ±inf, NaN and
@@ -136,8 +136,8 @@ def test_flat_chain_matches_unfused_ops_and_oracle(case):
 
 @pytest.mark.parametrize("n", [1, 3, 4, 5, 8, 255, 1024, 1027, 65536 * 4 + 12, 3 * (1 << 18) + 20])
 def test_flat_chain_sizes(n):
-    """Sizes around the streaming form's units, steps and per-workgroup ranges, and around the NEG
-    rule's 8-element SIMD blocks, on config 2's chain."""
+    """Sizes around the vector kernel's float4 units and two-unit lanes, and around the NEG rule's
+    8-element SIMD blocks, on config 2's chain."""
     from plast_amd import ops, runtime as rt
     name, nin, _, ins = TAPES[0]
     print(f"config-2 chain over {n}", flush=True)

@@ -2,7 +2,7 @@
 training step (the fused relu(X + b) chain, then grad_b = Σ_rows grad_Y through the split
 leading-axis reduction and its finalize) captured once and replayed several times, with fresh
 inputs uploaded eagerly between replays, each replay checked bit for bit against the same step
-run eagerly; plus a flat fused chain (2^20 elements, the streaming form), softmax with its backward and the one-pass
+run eagerly; plus a flat fused chain (2^20 elements, the tape interpreter), softmax with its backward and the one-pass
 epilogue captured and replayed, and the error paths (nested capture, a launch inside a capture,
 ending a capture that is not open)."""
 from __future__ import annotations
@@ -118,7 +118,7 @@ def test_fused_chain_replays():
     from plast_amd import ops
     rt = _rt()
     L = rt.lib()
-    print("graph: fused chain (streaming form)", flush=True)
+    print("graph: fused chain (tape interpreter)", flush=True)
     n = 1 << 20
     tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("MUL", 1, 1, 0, 0.0), ("ADD", 1, 2, 0, 0.0),
                           ("LEAKY_RELU", 0, 0, 0, 0.0), ("NEG", 0, 0, 0, 0.0),

@@ -1,5 +1,5 @@
 """Seeded random fused chains: random tapes (2-10 instructions over every op, operand source and
-operand order) over random layouts (flat, which runs the interpreter's streaming form; [rows, inner]
+operand order) over random layouts (flat, through the one-shot vector kernel; [rows, inner]
 with a bias row and per-row scalars; a transposed operand over whole or partial 64x64 tiles; and a
 small flat space). Each chain runs two ways on the GPU and both must agree bit for bit (NaN against
 NaN):

@@ -20,7 +20,10 @@ from plast_amd.abi import KernelParams
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(4, 10), (33, 1000), (8, 32000), (2, 3, 257), (1, 1), (5, 4096), (6, 9)]
+# (600, 2052) and (300, 8192) give the persistent forward more rows than workgroups, the first with
+# a partial last float4 unit per lane
+SHAPES = [(4, 10), (33, 1000), (8, 32000), (2, 3, 257), (1, 1), (5, 4096), (6, 9), (600, 2052),
+          (300, 8192)]
 
 
 def _x(shape, seed):
