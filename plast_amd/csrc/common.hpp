@@ -181,9 +181,6 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_STEP_BLOCK
 #define PLAST_CE_STEP_BLOCK 1024
 #endif
-#ifndef PLAST_CE_STEP_SETS
-#define PLAST_CE_STEP_SETS 2  // one-pass cross-entropy step: row register sets (rows in flight + 1)
-#endif
 #ifndef PLAST_CE_STEP_WPC
 #define PLAST_CE_STEP_WPC 1  // one-pass cross-entropy step: persistent workgroups per CU
 #endif

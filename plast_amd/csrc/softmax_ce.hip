@@ -512,8 +512,13 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // would wait for it too. Lanes past the row are masked where their values are used.
   // Addresses are a row base (uniform) plus a 32-bit byte offset per lane, which the loads and
   // stores take in one register (a 64-bit address per unit would take two).
-  auto load_row = [&](uint32_t r, f4 (&v)[V]) {
-    const char *xr = reinterpret_cast<const char *>(x + uint64_t(r < N ? r : N - 1) * C);
+  // The row's label and upstream gradient are loaded with it, a row ahead of their use (a load
+  // issued when the row's processing starts would stall it for a memory round trip).
+  auto load_row = [&](uint32_t r, f4 (&v)[V], int32_t &yl, float &gl) {
+    const uint32_t rc = r < N ? r : N - 1;
+    yl = lab[rc];
+    gl = dloss[rc];
+    const char *xr = reinterpret_cast<const char *>(x + uint64_t(rc) * C);
     const uint32_t ti = lane_index();
 #pragma unroll
     for (int u = 0; u < V; ++u) {
@@ -528,14 +533,12 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // e / S, within 2 ulp of it), with the one-hot term applied to the label's element alone. A
   // row's VALU work is then about 14 instructions per element, under the memory time (the
   // recomputed-exponential form took 36 and was issue-bound).
-  auto process = [&](uint32_t r, f4 (&v)[V]) {
+  auto process = [&](uint32_t r, f4 (&v)[V], const int32_t y, const float g) {
     // Consume every unit of the row here, on every path: a unit used only under a branch that some
     // waves skip (the row's ragged last unit) would leave its load pending past the loop's back
     // edge, and reusing its registers there would wait for every load, the prefetch included.
 #pragma unroll
     for (int u = 0; u < V; ++u) asm volatile("" ::"v"(v[u][0]), "v"(v[u][1]), "v"(v[u][2]), "v"(v[u][3]));
-    const float g = dloss[r];
-    const int32_t y = lab[r];
     const uint32_t ti = lane_index();
     const uint32_t full = C4 / BS;  // units every lane holds inside the row
     // round 1: the row's max and min (lanes past the row hold a copy of its last float4, which
@@ -657,33 +660,17 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // register a store of the previous row still reads, and that wait then leaves the prefetch alone
   // (with the stores last, it would wait for every load too).
   uint32_t r = blockIdx.x;
-  if constexpr (PLAST_CE_STEP_SETS == 3) {
-    // three sets: two rows in flight while one is processed
-    f4 xa[V], xb[V], xc[V];
-    load_row(r, xa);
-    load_row(r + G, xb);
-    load_row(r + 2 * G, xc);
-    for (; r < N; r += 3 * G) {
-      process(r, xa);
-      load_row(r + 3 * G, xa);
-      if (r + G >= N) break;
-      process(r + G, xb);
-      load_row(r + 4 * G, xb);
-      if (r + 2 * G >= N) break;
-      process(r + 2 * G, xc);
-      load_row(r + 5 * G, xc);
-    }
-  } else {
-    f4 xa[V], xb[V];
-    load_row(r, xa);
-    load_row(r + G, xb);
-    for (; r < N; r += 2 * G) {
-      process(r, xa);
-      load_row(r + 2 * G, xa);
-      if (r + G >= N) break;
-      process(r + G, xb);
-      load_row(r + 3 * G, xb);
-    }
+  f4 xa[V], xb[V];
+  int32_t ya, yb;
+  float ga, gb;
+  load_row(r, xa, ya, ga);
+  load_row(r + G, xb, yb, gb);
+  for (; r < N; r += 2 * G) {
+    process(r, xa, ya, ga);
+    load_row(r + 2 * G, xa, ya, ga);
+    if (r + G >= N) break;
+    process(r + G, xb, yb, gb);
+    load_row(r + 3 * G, xb, yb, gb);
   }
   f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(blockIdx.x) * C);
 #pragma unroll
