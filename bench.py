@@ -1,6 +1,7 @@
 """Benchmark of the MI355X elementwise / broadcast / reduction path (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c4r,...] [--no-cpu]
+    python bench.py --only KEYS --compare LIB1.so,LIB2.so   (builds timed against each other)
 
 Prints ONE JSON line. `value` is config 5 (the largest single-GPU
 config): a whole softmax-cross-entropy training step over [32768, 32000] fp32 logits - the forward's
@@ -69,6 +70,10 @@ class Workload:
     def step(self):
         ...
 
+    def rebind(self):
+        """Take the current build's entry points where setup() stored some (a graph's op slots);
+        the buffers stay."""
+
     def cpu(self):
         return None
 
@@ -98,6 +103,9 @@ class C2Fused(Workload):
         self.c = DeviceTensor((n,), zero=False).fill_("normal", 44, 0.0, 1.0)
         self.t = [DeviceTensor((n,), zero=False) for _ in range(4)]
         self.y = DeviceTensor((n,), zero=False)
+        self.rebind()
+
+    def rebind(self):
         g = Graph()
         m = g.node("mul", [self.a, self.b], self.t[0])
         s = g.node("add", [m, self.c], self.t[1])
@@ -196,15 +204,22 @@ class C1(Workload):
                                ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
 
         self.graph = None
-        if self.part == "graph":
-            # the forward and backward ops recorded once and replayed as one graph launch
-            self.eager_step()
-            L = lib()
-            if L.plast_hip_capture_begin() != 0:
-                raise SystemExit("bench.py: graph capture failed")
-            self.eager_step()
-            self.graph = L.plast_hip_capture_end()
-            L.check("capture")
+        self.rebind()
+
+    def rebind(self):
+        if self.part != "graph":
+            return
+        if self.graph:
+            self.graph_lib.plast_hip_graph_destroy(self.graph)
+            self.graph = None
+        # the forward and backward ops recorded once and replayed as one graph launch
+        self.eager_step()
+        L = self.graph_lib = lib()
+        if L.plast_hip_capture_begin() != 0:
+            raise SystemExit("bench.py: graph capture failed")
+        self.eager_step()
+        self.graph = L.plast_hip_capture_end()
+        L.check("capture")
 
     def eager_step(self):
         forward("fused_elementwise", [self.X, self.b], self.Y,
@@ -243,7 +258,7 @@ class C1(Workload):
 
     def free(self):
         if self.graph:
-            lib().plast_hip_graph_destroy(self.graph)
+            self.graph_lib.plast_hip_graph_destroy(self.graph)
             self.graph = None
         super().free()
 
@@ -730,6 +745,50 @@ def check_step(w: "C5Step", rows=64) -> dict:
     return worst
 
 
+def compare_builds(a) -> int:
+    """Library builds timed against each other in ONE process: the same box, the same process
+    state and the same input buffers (rates of one kernel differ by a few percent from one process
+    or box to the next, which a comparison across processes would mistake for the variants').
+    Seven passes over one set of buffers; in each, every build times every --only workload in
+    turn. Prints one JSON line: per build and workload, the GB/s of each pass and their median."""
+    from plast_amd.runtime import load_library, use_library
+    keys = [k for k in a.only.split(",") if k]
+    if not keys:
+        raise SystemExit("bench.py: --compare needs --only")
+    base = lib()
+    base.plast_hip_set_sync(0)
+    builds = []
+    for p in a.compare.split(","):
+        L = load_library(Path(p))
+        L.plast_hip_set_sync(0)
+        builds.append((Path(p).name, L))
+    # one set of buffers for every build: where the buffers land moves a kernel's rate by a few
+    # percent, so fresh allocations per build would mix that into the comparison
+    work = [detail_workloads()[k] for k in keys]
+    for w in work:
+        w.setup()
+    res = {tag: {w.name: [] for w in work} for tag, _ in builds}
+    try:
+        for _ in range(7):
+            for tag, L in builds:
+                use_library(L)
+                for w in work:
+                    w.rebind()
+                    steps = max(a.steps, w.min_steps)
+                    ms = timed(w.step, steps, max(a.warmup, 2))
+                    res[tag][w.name].append(round(w.bytes_per_call / (ms * 1e-3) / 1e9, 1))
+                    log(f"{tag} {w.name}: {res[tag][w.name][-1]} GB/s")
+    finally:
+        use_library(base)
+        for w in work:
+            w.rebind()
+            w.free()
+    print(json.dumps({"compare": {tag: {n: {"GB_s": v, "median": float(np.median(v))}
+                                        for n, v in r.items()} for tag, r in res.items()}}),
+          flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -738,11 +797,16 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default="", help="comma list of detail keys (default: all)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--compare", default="",
+                    help="comma list of library builds (plast_amd.build --out): time the --only "
+                         "workloads with each in turn in this process and print their medians")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no collective or multi-GPU path is "
               "built); run with --gpus 1", file=sys.stderr)
         return 2
+    if a.compare:
+        return compare_builds(a)
     cores = host_cores()
     # the reference's CPU kernels use OpenMP: every online core of this host, stated in the line
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))

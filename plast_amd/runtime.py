@@ -130,6 +130,26 @@ def lib() -> Library:
     return _LIB
 
 
+def load_library(path: Path) -> Library:
+    """Another build of the library (a variant built with `plast_amd.build --out`), loaded beside
+    the current one and initialised on the same device. Each build keeps its own state (stream,
+    workspaces, errors); device memory is the process's, so tensors allocated through one build
+    can be passed to another's entry points."""
+    L = Library(Path(path))
+    if L.plast_hip_init(int(os.environ.get("PLAST_HIP_DEVICE", "0"))) != 0:
+        L.check("plast_hip_init")
+    return L
+
+
+def use_library(L: Library) -> Library:
+    """Make lib() return L from now on (for timing builds against each other in one process);
+    returns the build it replaces."""
+    global _LIB
+    prev = lib()
+    _LIB = L
+    return prev
+
+
 def _row_major(shape) -> tuple[int, ...]:
     st, acc = [], 1
     for e in reversed(shape):
