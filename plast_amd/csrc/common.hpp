@@ -181,6 +181,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_STEP_BLOCK
 #define PLAST_CE_STEP_BLOCK 1024
 #endif
+// The cross-entropy forward op keeps one wave per row: the one-pass step's row loop without its
+// gradient (persistent 1024-lane workgroups) measured 5.85 TB/s against 6.52 over [32768, 32000]
+// in one process and was removed.
 #ifndef PLAST_CE_STEP_WPC
 #define PLAST_CE_STEP_WPC 1  // one-pass cross-entropy step: persistent workgroups per CU
 #endif

@@ -680,23 +680,36 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   }
 }
 
-// dbias[c] = sum over workgroups b = 0 .. G-1 of part[b][c], in that order, one lane per column
-// with the loads of each batch of 16 issued before their adds.
+// dbias[c] = the sum over workgroups b = 0 .. G-1 of part[b][c], deterministically: a workgroup
+// takes 32 columns; its lane group q (of 8) sums the q-th eighth of the b range in order (32 lanes
+// read 32 adjacent columns, 128 B, per row), then lane c adds the 8 group sums in q order.
+constexpr int kFinCols = 32, kFinGroups = kCeBlock / kFinCols;
 __global__ __launch_bounds__(kCeBlock) void ce_step_finalize(const float *__restrict__ part,
                                                              float *__restrict__ dbias, uint32_t C,
                                                              uint32_t G) {
-  const uint32_t c = blockIdx.x * kCeBlock + threadIdx.x;
-  if (c >= C) return;
+  __shared__ float sh[kFinGroups][kFinCols];
+  const uint32_t cl = threadIdx.x % kFinCols, q = threadIdx.x / kFinCols;
+  const uint32_t c = blockIdx.x * kFinCols + cl;
+  const uint32_t per = (G + kFinGroups - 1) / kFinGroups;
+  const uint32_t b0 = q * per, b1 = b0 + per < G ? b0 + per : G;
   float s = 0.0f;
-  for (uint32_t b0 = 0; b0 < G; b0 += 16) {
-    float v[16];
+  if (c < C) {
+    for (uint32_t b = b0; b < b1; b += 8) {
+      float v[8];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = b0 + k < G ? part[uint64_t(b0 + k) * C + c] : 0.0f;
+      for (int k = 0; k < 8; ++k) v[k] = b + k < b1 ? part[uint64_t(b + k) * C + c] : 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-      if (b0 + k < G) s += v[k];
+      for (int k = 0; k < 8; ++k)
+        if (b + k < b1) s += v[k];
+    }
   }
-  dbias[c] = s;
+  sh[q][cl] = s;
+  __syncthreads();
+  if (q != 0 || c >= C) return;
+  float t = sh[0][cl];
+#pragma unroll
+  for (int g = 1; g < kFinGroups; ++g) t += sh[g][cl];
+  dbias[c] = t;
 }
 
 // Whether ce_step_kernel<V> may be launched with its dynamic LDS (raising its limit once: beyond
@@ -775,7 +788,7 @@ void ce_step_launch(int V, unsigned grid, float *part, const float *logits, cons
                     uint64_t N, uint64_t C) {
   const uint32_t c32 = uint32_t(C);
   ce_step_launch_v<1>(V, grid, part, logits, labels, dloss, stats, loss, dlogits, uint32_t(N), c32);
-  if (dbias) ce_step_finalize<<<ceil_div(C, kCeBlock), kCeBlock, 0, stream()>>>(part, dbias, c32, grid);
+  if (dbias) ce_step_finalize<<<ceil_div(C, kFinCols), kCeBlock, 0, stream()>>>(part, dbias, c32, grid);
 }
 
 bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
