@@ -206,13 +206,20 @@ __device__ __forceinline__ void store_final(void *out, int64_t off, const typena
 
 // ------------------------------------------------------------------------- rows kernel
 
+// The i-th term of a serial refold. A storing producer's terms are read back from where it stored
+// them (only a sum over a leading axis refolds one, after its workgroup or launch has stored every
+// term of the column): its inputs may have been overwritten by those stores (dc written over dout).
 template <class Prod, int NIN>
 __device__ __forceinline__ float value_at(const RedArgs<NIN> &A, const Prod &prod,
                                           const int64_t *base, uint64_t i) {
-  float v[NIN];
+  if constexpr (kStores<Prod>) {
+    return prod.dst[base[0] + int64_t(i) * A.rst[0]];
+  } else {
+    float v[NIN];
 #pragma unroll
-  for (int k = 0; k < NIN; ++k) v[k] = A.in[k][base[k] + int64_t(i) * A.rst[k]];
-  return prod.eval(v);
+    for (int k = 0; k < NIN; ++k) v[k] = A.in[k][base[k] + int64_t(i) * A.rst[k]];
+    return prod.eval(v);
+  }
 }
 
 template <class T>

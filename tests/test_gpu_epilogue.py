@@ -105,6 +105,32 @@ def test_gpu_fused_modulate_bias_grad_unaligned_and_in_place():
     assert (E.numpy() == 0.0).all() and not np.signbit(E.numpy()).any()
 
 
+@pytest.mark.parametrize("M,N", [(96, 64), (4096, 1024)], ids=["one-launch", "chunked"])
+def test_gpu_fused_in_place_refold_reads_the_stored_terms(M, N):
+    """A column whose sum is not finite is summed again in index order. With dc written over dout,
+    the terms must be read back as stored: re-modulating the overwritten inputs would scale the
+    out <= 0 terms by alpha twice. Column 1 holds three 1.5e38 terms (3e38 with out < 0, alpha 0.5)
+    and then -inf: index order gives inf + -inf = NaN, the doubly scaled terms -inf. Checked
+    against the two calls (modulation into a separate buffer, then the column sum), bit for bit,
+    for the one-launch small sum and the chunked sum with its finalize."""
+    from plast_amd import runtime as rt
+    L = rt.lib()
+    alpha = 0.5
+    dout, out = epilogue_inputs(M, N, 11)
+    dout[:3, 1] = 3e38
+    out[:3, 1] = -1.0
+    dout[5, 1] = -np.inf
+    out[5, 1] = 1.0
+    D, O = rt.DeviceTensor.from_numpy(dout), rt.DeviceTensor.from_numpy(out)
+    wdc, wdb = _two_step(L, D.ptr, O.ptr, M, N, alpha)
+    assert np.isnan(wdb[1])
+    DB = rt.DeviceTensor((N,), zero=False)
+    L.relu_grad_modulate_bias_grad_hip(D.ptr, O.ptr, D.ptr, DB.ptr, M * N, N, alpha)
+    L.check("fused, in place")
+    assert_bits(D.numpy(), wdc, "dc over dout")
+    assert_bits(DB.numpy(), wdb, "dbias, in place")
+
+
 def test_gpu_bias_grad_rejects_ragged_rows():
     from plast_amd import runtime as rt
     L = rt.lib()
