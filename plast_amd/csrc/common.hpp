@@ -106,6 +106,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_NT_STORE
 #define PLAST_CE_NT_STORE 1
 #endif
+#ifndef PLAST_ROW_BLOCKED
+#define PLAST_ROW_BLOCKED 0  // persistent row kernels: rows strided over the grid (0) or blocked (1)
+#endif
+#ifndef PLAST_CE_STEP_NT_LOAD
+#define PLAST_CE_STEP_NT_LOAD 1  // the one-pass step's row loads: nontemporal (1) or ordinary (0)
+#endif
 #ifndef PLAST_COPY_NT_STORE
 #define PLAST_COPY_NT_STORE 0
 #endif

@@ -447,6 +447,30 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // the G rows of part in workgroup order. No atomics: the bias gradient is deterministic for a
 // given grid. Registers hold the two row sets only (the column sums there would spill at 1024
 // lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
+// The rows a persistent row kernel's workgroup walks: r, r + S, ... below rend. Strided
+// (PLAST_ROW_BLOCKED 0): rows b, b + G, ..., so the grid sweeps the tensor front to back;
+// blocked (1): a contiguous block of ceil(N / G) rows per workgroup.
+__device__ __forceinline__ void row_range(uint32_t N, uint32_t G, uint32_t &r, uint32_t &S,
+                                          uint32_t &rend) {
+  if constexpr (PLAST_ROW_BLOCKED) {
+    const uint32_t per = (N + G - 1) / G;
+    r = blockIdx.x * per;
+    rend = r + per < N ? r + per : N;
+    S = 1;
+  } else {
+    r = blockIdx.x;
+    rend = N;
+    S = G;
+  }
+}
+
+// A row unit of the persistent row kernels: nontemporal (NT) or ordinary load.
+template <bool NT>
+__device__ __forceinline__ f4 load_row_unit(const f4 *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
 constexpr int kStepBlock = PLAST_CE_STEP_BLOCK;
 // The widest row the LDS column sums allow: a float4 slot per lane and unit within 159 KiB of a
 // CU's 160 (1024 lanes: 8 units, rows up to 32768 floats; 512 lanes: 16 units, 65536 floats).
@@ -524,7 +548,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     for (int u = 0; u < V; ++u) {
       const uint32_t q = ti + uint32_t(u) * BS;
       const uint32_t off = (q < C4 ? q : C4 - 1) * 16u;
-      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + off));
+      v[u] = load_row_unit<PLAST_CE_STEP_NT_LOAD>(reinterpret_cast<const f4 *>(xr + off));
     }
   };
 
@@ -659,18 +683,19 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // youngest memory operations at the loop's back edge are loads: the loop head may reuse a
   // register a store of the previous row still reads, and that wait then leaves the prefetch alone
   // (with the stores last, it would wait for every load too).
-  uint32_t r = blockIdx.x;
+  uint32_t r, S, rend;
+  row_range(N, G, r, S, rend);
   f4 xa[V], xb[V];
   int32_t ya, yb;
   float ga, gb;
   load_row(r, xa, ya, ga);
-  load_row(r + G, xb, yb, gb);
-  for (; r < N; r += 2 * G) {
+  load_row(r + S, xb, yb, gb);
+  for (; r < rend; r += 2 * S) {
     process(r, xa, ya, ga);
-    load_row(r + 2 * G, xa, ya, ga);
-    if (r + G >= N) break;
-    process(r + G, xb, yb, gb);
-    load_row(r + 3 * G, xb, yb, gb);
+    load_row(r + 2 * S, xa, ya, ga);
+    if (r + S >= rend) break;
+    process(r + S, xb, yb, gb);
+    load_row(r + 3 * S, xb, yb, gb);
   }
   f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(blockIdx.x) * C);
 #pragma unroll
@@ -1029,16 +1054,17 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
       }
     }
   };
-  uint32_t r = blockIdx.x;
+  uint32_t r, S, rend;
+  row_range(N, G, r, S, rend);
   f4 xa[V], xb[V];
   load_row(r, xa);
-  load_row(r + G, xb);
-  for (; r < N; r += 2 * G) {
+  load_row(r + S, xb);
+  for (; r < rend; r += 2 * S) {
     process(r, xa);
-    load_row(r + 2 * G, xa);
-    if (r + G >= N) break;
-    process(r + G, xb);
-    load_row(r + 3 * G, xb);
+    load_row(r + 2 * S, xa);
+    if (r + S >= rend) break;
+    process(r + S, xb);
+    load_row(r + 3 * S, xb);
   }
 }
 
