@@ -130,3 +130,31 @@ def test_softmax_rejects_other_axes():
     y = rt.DeviceTensor((3, 4), zero=False)
     with pytest.raises(rt.PlastHipError, match="last axis"):
         rt.forward("softmax", [x], y, KernelParams(0, 0, 0.0))
+
+
+def test_softmax_full_size_properties():
+    """The persistent forward at the benchmarked [32768, 32000], through size-independent
+    properties checked on the device with the library's own pinned reductions: every softmax row
+    sums to 1, every exp(log-softmax) row sums to 1 (within 32000 terms' fp32 rounding plus the
+    exponential's error), and each row's argmax is the argmax of its logits (softmax is monotonic;
+    ties are vanishingly unlikely for N(0, 2) logits)."""
+    from plast_amd import ops, runtime as rt
+    print("softmax at [32768, 32000]", flush=True)
+    N, Cn = 32768, 32000
+    x = rt.DeviceTensor((N, Cn), zero=False).fill_("normal", 21, 0.0, 2.0)
+    y = rt.DeviceTensor((N, Cn), zero=False)
+    try:
+        rt.forward("softmax", [x], y, KernelParams(1, 0, 0.0))
+        s = ops.reduce("sum", y, dim=1).numpy()
+        assert np.all(np.abs(s.astype(np.float64) - 1.0) <= 2e-4), f"row sums {s.min()}..{s.max()}"
+        ax, ay = ops.reduce("argmax", x, dim=1).numpy(), ops.reduce("argmax", y, dim=1).numpy()
+        assert np.array_equal(ax, ay), f"{int((ax != ay).sum())} rows change their argmax"
+        rt.forward("log_softmax", [x], y, KernelParams(1, 0, 0.0))
+        e = rt.DeviceTensor((N, Cn), zero=False)
+        rt.forward("exp", [y], e)
+        s = ops.reduce("sum", e, dim=1).numpy()
+        e.free()
+        assert np.all(np.abs(s.astype(np.float64) - 1.0) <= 2e-4), f"exp row sums {s.min()}..{s.max()}"
+    finally:
+        x.free()
+        y.free()
