@@ -213,12 +213,16 @@ class C1(Workload):
             self.graph_lib.plast_hip_graph_destroy(self.graph)
             self.graph = None
         # the forward and backward ops recorded once and replayed as one graph launch
+        import gc
         self.eager_step()
+        gc.collect()
         L = self.graph_lib = lib()
         if L.plast_hip_capture_begin() != 0:
             raise SystemExit("bench.py: graph capture failed")
-        self.eager_step()
-        self.graph = L.plast_hip_capture_end()
+        try:
+            self.eager_step()
+        finally:
+            self.graph = L.plast_hip_capture_end()
         L.check("capture")
 
     def eager_step(self):
@@ -242,13 +246,17 @@ class C1(Workload):
         calls). None for the graph workload itself."""
         if self.part not in ("fwd", "bwd"):
             return None
+        import gc
         L = lib()
         self.step()  # sizes the workspaces outside the capture
+        gc.collect()  # no tensor of an earlier workload is freed inside the capture
         if L.plast_hip_capture_begin() != 0:
             raise SystemExit("bench.py: graph capture failed")
-        for _ in range(calls):
-            self.step()
-        g = L.plast_hip_capture_end()
+        try:
+            for _ in range(calls):
+                self.step()
+        finally:
+            g = L.plast_hip_capture_end()
         L.check("capture")
         try:
             ms = timed(lambda: L.plast_hip_graph_launch(g), reps, 2)
@@ -257,7 +265,7 @@ class C1(Workload):
         return round(ms * 1e3 / calls, 2)
 
     def free(self):
-        if self.graph:
+        if getattr(self, "graph", None):
             self.graph_lib.plast_hip_graph_destroy(self.graph)
             self.graph = None
         super().free()

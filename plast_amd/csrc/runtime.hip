@@ -2,6 +2,7 @@
 // reference's L0/L1 layer, timing marks, deterministic input generation and the copy ceiling.
 #include <cstdarg>
 #include <cstdlib>
+#include <vector>
 
 #include "common.hpp"
 #include "ws_ledger.hpp"
@@ -18,6 +19,7 @@ int g_err_count = 0;
 char g_err_msg[512] = "";
 constexpr int kSlots = 3;
 WorkspaceLedger<kSlots> g_ws;  // workspace slots, and the graphs captured over them
+std::vector<void *> g_deferred_frees;  // arena_free_hip calls made while capturing
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
 int g_cus = 256;  // compute units of the device (MI355X: 256), read at init
 }  // namespace
@@ -74,6 +76,14 @@ void finish(const char *where) {
 static void release_workspace(void *p) {
   (void)hipStreamSynchronize(g_stream);
   (void)hipFree(p);
+}
+
+// Frees the buffers arena_free_hip was given during a capture (called once it has ended).
+static void release_deferred_frees() {
+  if (g_deferred_frees.empty()) return;
+  (void)hipStreamSynchronize(g_stream);
+  for (void *p : g_deferred_frees) (void)hipFree(p);
+  g_deferred_frees.clear();
 }
 
 void *workspace(size_t bytes, int slot) {
@@ -329,6 +339,7 @@ void *plast_hip_capture_end(void) {
   g_capturing = false;
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(g_stream, &graph);
+  release_deferred_frees();
   if (e != hipSuccess || !graph) {
     report_error("plast_hip_capture_end", "%s", hipGetErrorString(e));
     return nullptr;
@@ -434,6 +445,12 @@ void *arena_alloc_hip(u64 size) {
 
 void arena_free_hip(void *ptr) {
   if (!ptr || !ensure_init()) return;
+  if (g_capturing) {
+    // neither a wait nor hipFree may happen while the stream records (either would invalidate
+    // the capture): the buffer is freed when the capture ends
+    g_deferred_frees.push_back(ptr);
+    return;
+  }
   PLAST_HIP_TRY("arena_free_hip", hipStreamSynchronize(g_stream));
   PLAST_HIP_TRY("arena_free_hip", hipFree(ptr));
 }

@@ -174,17 +174,20 @@ def test_capture_errors():
 
 
 def test_workspace_outgrown_while_a_graph_lives():
-    """Config 1's step (its grad_b partial sums in workspace slot 0) captured; then eager work grows
-    slot 0 (a reserve past its size, then a cross-entropy step whose partial sums need more): the
-    outgrown buffers are retired, not freed, so every replay still reads and writes the buffer it
-    was recorded with and matches the eager step bit for bit; destroying the graph frees them."""
+    """A captured step whose leading-axis sum keeps its chunk partials in workspace slot 0 (a
+    [4096, 1024] sum, large enough for the chunked path), beside config 1's fused forward; then
+    eager work grows slot 0 (a reserve past its size, then a cross-entropy step whose partial sums
+    need more): the outgrown buffers are retired, not freed, so every replay still reads and writes
+    the buffer it was recorded with and matches the eager step bit for bit; destroying the graph
+    frees them."""
     from plast_amd import abi, ops
     from plast_amd.abi import KernelParams
     rt = _rt()
     L = rt.lib()
     print("graph: workspace outgrown while the graph lives", flush=True)
-    X, b, gy = (rt.DeviceTensor(s, zero=False) for s in ((1024, 256), (256,), (1024, 256)))
-    Y, gb = rt.DeviceTensor((1024, 256), zero=False), rt.DeviceTensor((256,), zero=False)
+    X, b = (rt.DeviceTensor(s, zero=False) for s in ((1024, 256), (256,)))
+    Y = rt.DeviceTensor((1024, 256), zero=False)
+    gy, gb = rt.DeviceTensor((4096, 1024), zero=False), rt.DeviceTensor((1024,), zero=False)
     tape = ops.make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
                           ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
 
@@ -195,15 +198,18 @@ def test_workspace_outgrown_while_a_graph_lives():
     rng = np.random.RandomState(3)
 
     def fresh():
-        for t, shape in ((X, (1024, 256)), (b, (256,)), (gy, (1024, 256))):
+        for t, shape in ((X, (1024, 256)), (b, (256,)), (gy, (4096, 1024))):
             _h2d(t, rng.uniform(-1, 1, shape))
 
     fresh()
-    step()
+    step()                                   # the sum sizes slot 0 outside the capture
+    assert L.plast_hip_workspace_bytes(0) > 0
     alive0, retired0 = L.plast_hip_graphs_alive(), L.plast_hip_workspace_retired()
     assert L.plast_hip_capture_begin() == 0
-    step()
-    graph = L.plast_hip_capture_end()
+    try:
+        step()
+    finally:
+        graph = L.plast_hip_capture_end()
     L.check("capture")
     assert graph and L.plast_hip_graphs_alive() == alive0 + 1
     try:
@@ -214,12 +220,12 @@ def test_workspace_outgrown_while_a_graph_lives():
         assert L.plast_hip_workspace_retired() == retired0 + 1
         # a cross-entropy step whose 256 workgroups' column sums outgrow slot 0 again
         N, Cn = 512, 4 * (L.plast_hip_workspace_bytes(0) // (256 * 4 * 4) + 1)
-        logits = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 7, -2.0, 2.0)
-        labels = rt.DeviceTensor.from_numpy(rng.randint(0, Cn, N).astype(np.int32))
-        dloss = rt.DeviceTensor.from_numpy(np.full(N, 1.0 / N, np.float32))
-        st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
-        dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
         if Cn <= 32768:
+            logits = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 7, -2.0, 2.0)
+            labels = rt.DeviceTensor.from_numpy(rng.randint(0, Cn, N).astype(np.int32))
+            dloss = rt.DeviceTensor.from_numpy(np.full(N, 1.0 / N, np.float32))
+            st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
+            dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
             L.softmax_cross_entropy_step_hip(logits.ptr, labels.ptr, dloss.ptr, st.ptr, loss.ptr,
                                              dx.ptr, db.ptr, N, Cn)
             L.check("ce step")
@@ -230,9 +236,43 @@ def test_workspace_outgrown_while_a_graph_lives():
             y_g, gb_g = Y.numpy(), gb.numpy()
             step()                           # eagerly, through the grown slot
             assert_bits(y_g, Y.numpy(), f"replay {rep}: relu(X + b)")
-            assert_bits(gb_g, gb.numpy(), f"replay {rep}: grad_b")
+            assert_bits(gb_g, gb.numpy(), f"replay {rep}: column sum")
     finally:
         L.plast_hip_graph_destroy(graph)
     assert L.plast_hip_graphs_alive() == alive0
     if alive0 == 0:
         assert L.plast_hip_workspace_retired() == 0
+
+
+def test_free_during_capture_is_deferred():
+    """A tensor freed while a graph is being recorded (Python may collect one at any time): the
+    free is deferred to the end of the capture instead of waiting on the recording stream, so the
+    capture stays valid and its replays match the eager op."""
+    rt = _rt()
+    L = rt.lib()
+    print("graph: free during capture", flush=True)
+    x = rt.DeviceTensor((4096,), zero=False)
+    y = rt.DeviceTensor((4096,), zero=False)
+    doomed = rt.DeviceTensor((1 << 20,), zero=False)
+    rng = np.random.RandomState(5)
+    _h2d(x, rng.randn(4096))
+    rt.forward("neg", [x], y)
+    L.plast_hip_clear_error()
+    assert L.plast_hip_capture_begin() == 0
+    try:
+        rt.forward("neg", [x], y)
+        doomed.free()                                   # deferred, not an error
+        assert L.plast_hip_error_count() == 0
+    finally:
+        graph = L.plast_hip_capture_end()
+    L.check("capture with a free inside")
+    assert graph
+    try:
+        for rep in range(3):
+            _h2d(x, rng.randn(4096))
+            assert L.plast_hip_graph_launch(graph) == 0
+            got = y.numpy()
+            rt.forward("neg", [x], y)
+            assert_bits(got, y.numpy(), f"replay {rep}")
+    finally:
+        L.plast_hip_graph_destroy(graph)
