@@ -169,6 +169,11 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // maxima and sums merged after it) 5.81 TB/s against 5.89 for two; the backward with the input
 // gradient's loads issued with y and dy 5.64 against 5.62-5.64 without, and 5.54-5.65 at 1024
 // lanes. Neither was kept.
+// Softmax backward: the input gradient's read-modify-write nontemporal (1) or ordinary (0).
+// Measured at [32768, 32000] in one process: 5.96 TB/s against 5.61.
+#ifndef PLAST_SOFTMAX_BWD_NT
+#define PLAST_SOFTMAX_BWD_NT 1
+#endif
 // Softmax backward, rows held in registers: lanes per row.
 #ifndef PLAST_SOFTMAX_BWD_BLOCK
 #define PLAST_SOFTMAX_BWD_BLOCK 512

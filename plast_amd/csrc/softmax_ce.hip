@@ -1125,11 +1125,11 @@ __global__ __launch_bounds__(BS) void softmax_bwd_reg_kernel(const float *__rest
   for (int u = 0; u < V; ++u) {
     const uint32_t q = threadIdx.x + uint32_t(u) * BS;
     if (q >= C4) continue;
-    f4 d = d4[q];
+    f4 d = PLAST_SOFTMAX_BWD_NT ? __builtin_nontemporal_load(d4 + q) : d4[q];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       d[c] = d[c] + (LOG ? gv[u][c] - expf(yv[u][c]) * t : yv[u][c] * (gv[u][c] - t));
-    d4[q] = d;
+    store_stream<PLAST_SOFTMAX_BWD_NT>(d, d4 + q);
   }
 }
 
