@@ -56,6 +56,27 @@ def timed(fn, steps: int, warmup: int) -> float:
     return ms / steps
 
 
+class BenchCall(C.Structure):
+    """One entry-point call for bench_calls.c's bench_call_loop (same field layout)."""
+    _fields_ = [("fn", C.c_void_p), ("inputs", C.c_void_p), ("output", C.c_void_p),
+                ("params", KernelParams)]
+
+
+_HELPER: list = []
+
+
+def bench_helper():
+    """bench_calls.so (built by plast_amd/build.py:build_bench_helper), or None when absent."""
+    if not _HELPER:
+        p = ROOT / "bench_calls.so"
+        h = C.CDLL(str(p)) if p.exists() else None
+        if h is not None:
+            h.bench_call_loop.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+            h.bench_call_loop.restype = C.c_double
+        _HELPER.append(h)
+    return _HELPER[0]
+
+
 # ----------------------------------------------------------------------------- workloads
 class Workload:
     name = ""
@@ -230,15 +251,46 @@ class C1(Workload):
                 KernelParams(C.addressof(self.tape), 0, 0.0))
         forward("sum", [self.gy], self.gb, KernelParams(0, 0, 0.0))
 
-    def step(self):
+    def call(self):
+        """(op, inputs, output, params) of the one entry-point call a step of fwd, big or bwd is."""
         if self.part in ("fwd", "big"):
-            forward("fused_elementwise", [self.X, self.b], self.Y,
+            return ("fused_elementwise", [self.X, self.b], self.Y,
                     KernelParams(C.addressof(self.tape), 0, 0.0))
-        elif self.part == "bwd":
-            forward("sum", [self.gy], self.gb, KernelParams(0, 0, 0.0))
-        else:
+        return "sum", [self.gy], self.gb, KernelParams(0, 0, 0.0)
+
+    def step(self):
+        if self.part == "graph":
             if lib().plast_hip_graph_launch(self.graph) != 0:
                 raise SystemExit("bench.py: graph launch failed")
+        else:
+            forward(*self.call())
+
+    def c_us(self, calls: int = 20000, reps: int = 3):
+        """Wall microseconds per call when a C loop (bench_calls.c) makes the calls back to back,
+        the library asynchronous and its stream drained at the end: what a C caller such as the
+        reference's executor pays per call, without Python's cost. Best of `reps` loops; None for
+        the graph and big workloads or without bench_calls.so."""
+        h = bench_helper()
+        if h is None or self.part not in ("fwd", "bwd"):
+            return None
+        L = lib()
+        name, ins, out, p = self.call()
+        arr = (abi.TensorP * len(ins))(*[x.p for x in ins])
+        bc = BenchCall(C.cast(L.entry["forward", name], C.c_void_p).value, C.addressof(arr),
+                       C.addressof(out.t), p)
+        sync = C.cast(L._L.plast_hip_synchronize, C.c_void_p).value
+        errors = C.cast(L._L.plast_hip_error_count, C.c_void_p).value
+        L.plast_hip_synchronize()
+        best = None
+        for i in range(reps + 1):  # the first loop warms up
+            n = calls // 10 if i == 0 else calls
+            us = h.bench_call_loop(C.byref(bc), 1, n, sync, errors)
+            if us < 0:
+                L.check("bench_call_loop")
+                raise SystemExit("bench.py: the C call loop failed")
+            if i:
+                best = us / n if best is None else min(best, us / n)
+        return round(best, 2)
 
     def kernel_us(self, calls: int = 100, reps: int = 5):
         """Device microseconds per call without the host's per-call cost: `calls` back-to-back
@@ -702,11 +754,15 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     r = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
          "elems_per_s": round(w.elems / (ms * 1e-3), 1), "algorithmic_bytes": w.bytes_per_call}
     if isinstance(w, C1) and w.part != "big":
-        # latency-bound: microseconds per call as the caller sees them, and on the device alone
+        # latency-bound: microseconds per call as a Python caller and a C caller see them, and on
+        # the device alone
         r["us_per_call"] = round(ms * 1e3, 2)
         k = w.kernel_us()
         if k is not None:
             r["kernel_us_per_call"] = k
+        c = w.c_us()
+        if c is not None:
+            r["c_caller_us_per_call"] = c
     return r
 
 

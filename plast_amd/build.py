@@ -86,6 +86,17 @@ def build_library(jobs: int | None = None, defines: list[str] | None = None,
     return lib
 
 
+def build_bench_helper() -> Path:
+    """bench_calls.so: bench.py's C loop that times entry-point calls without Python (gcc; it links
+    nothing and runs no GPU code of its own)."""
+    out = ROOT / "bench_calls.so"
+    tmp = out.with_suffix(".so.tmp")
+    _run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", f"-I{ROOT / 'include'}",
+          str(ROOT / "bench_calls.c"), "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
 def build_oracle() -> None:
     """Test infrastructure: the C restatement and, when /root/reference exists, the reference."""
     make = shutil.which("make") or "make"
@@ -103,6 +114,8 @@ def main(argv: list[str] | None = None) -> int:
     if a.defines and not a.out:
         ap.error("-D builds a variant: give it --out so the in-tree library stays the default")
     print(build_library(a.j, a.defines, a.out))
+    if not a.out:
+        print(build_bench_helper())
     if a.oracle:
         build_oracle()
     return 0

@@ -39,11 +39,14 @@ class Library:
         self.path = str(path)
         L = C.CDLL(self.path)
         self._L = L
+        # (kind, op name) -> bound entry point, looked up once: the per-call path does no
+        # attribute lookups or string formatting
+        self.entry = {}
         for name in OP_NAMES:
-            f = getattr(L, f"{name}_hip_forward")
-            f.argtypes, f.restype = [TensorPP, TensorP, KernelParams], None
-            b = getattr(L, f"{name}_hip_backward")
-            b.argtypes, b.restype = [TensorPP, TensorP, KernelParams], None
+            for kind in ("forward", "backward"):
+                f = getattr(L, f"{name}_hip_{kind}")
+                f.argtypes, f.restype = [TensorPP, TensorP, KernelParams], None
+                self.entry[kind, name] = f
         sig = {
             "plast_hip_init": ([C.c_int], C.c_int),
             "plast_hip_set_sync": ([C.c_int], None),
@@ -106,16 +109,20 @@ class Library:
         for name, (args, res) in sig.items():
             f = getattr(L, name)
             f.argtypes, f.restype = args, res
+        self.error_count = L.plast_hip_error_count
 
     def __getattr__(self, name):
         return getattr(self._L, name)
 
     def check(self, what: str = "") -> None:
         """Raise if the library reported an error since the last check."""
-        if self._L.plast_hip_error_count():
-            msg = self._L.plast_hip_last_error().decode()
-            self._L.plast_hip_clear_error()
-            raise PlastHipError(f"{what}: {msg}" if what else msg)
+        if self.error_count():
+            self.raise_error(what)
+
+    def raise_error(self, what: str = "") -> None:
+        msg = self._L.plast_hip_last_error().decode()
+        self._L.plast_hip_clear_error()
+        raise PlastHipError(f"{what}: {msg}" if what else msg)
 
 
 _LIB: Library | None = None
@@ -183,6 +190,7 @@ class DeviceTensor:
             self.grad = DeviceTensor(self.shape, dtype, strides=strides)
         self.t = abi.make_tensor(self.ptr, self.shape, strides, dtype, GPU, requires_grad,
                                  self.grad.t if self.grad is not None else None)
+        self.p = C.pointer(self.t)  # what the entry points take; built once
         if zero and self._own:
             L.zeros_hip(C.byref(self.t), n)
             L.check("zeros_hip")
@@ -252,13 +260,20 @@ class DeviceTensor:
             pass
 
 
+_PTR_ARRAY = [TensorP * n for n in range(17)]
+
+
+def _ptr(x) -> TensorP:
+    return x.p if isinstance(x, DeviceTensor) else C.pointer(x)
+
+
 def _call(kind: str, name: str, inputs, output, p: KernelParams):
     L = lib()
-    arr = (TensorP * len(inputs))(*[C.pointer(x.t if isinstance(x, DeviceTensor) else x)
-                                    for x in inputs])
-    out = output.t if isinstance(output, DeviceTensor) else output
-    getattr(L, f"{name}_hip_{kind}")(C.cast(arr, TensorPP), C.byref(out), p)
-    L.check(f"{name}_hip_{kind}")
+    n = len(inputs)
+    arr = (_PTR_ARRAY[n] if n < len(_PTR_ARRAY) else TensorP * n)(*map(_ptr, inputs))
+    L.entry[kind, name](arr, _ptr(output), p)
+    if L.error_count():
+        L.raise_error(f"{name}_hip_{kind}")
 
 
 def forward(name: str, inputs, output, p: KernelParams | None = None) -> None:
