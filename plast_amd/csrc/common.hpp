@@ -114,6 +114,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_ROW_BLOCKED
 #define PLAST_ROW_BLOCKED 0  // persistent row kernels: rows strided over the grid (0) or blocked (1)
 #endif
+// Persistent row kernels: workgroup numbers renumbered so that each XCD holds a contiguous range
+// (1) or dispatch order (0). Measured in one process: softmax forward 5947 against 5920 GB/s, the
+// one-pass step unchanged (5759 / 5760).
+#ifndef PLAST_ROW_XCD
+#define PLAST_ROW_XCD 1
+#endif
 #ifndef PLAST_CE_STEP_NT_LOAD
 #define PLAST_CE_STEP_NT_LOAD 1  // the one-pass step's row loads: nontemporal (1) or ordinary (0)
 #endif
@@ -193,7 +199,9 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #define PLAST_CE_BWD_BLOCK 256  // cross-entropy backward, flat form: workgroup size
 #endif
 // One-pass cross-entropy step: lanes per workgroup (one row). Measured on config 5's step (two
-// alternating runs): 1024 lanes x 8 float4 (119 VGPRs) 5.68-5.70 TB/s, 512 x 16 (189) 5.50.
+// alternating runs): 1024 lanes x 8 float4 (119 VGPRs) 5.68-5.70 TB/s, 512 x 16 (189) 5.50. In
+// one process: 1024 x 8 with two register sets 5760, 512 x 16 with two 5559, 512 x 16 with three
+// (254 VGPRs, two rows in flight while one is processed) 5565, and 5623 with the XCD numbering.
 #ifndef PLAST_CE_STEP_BLOCK
 #define PLAST_CE_STEP_BLOCK 1024
 #endif

@@ -447,18 +447,27 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // the G rows of part in workgroup order. No atomics: the bias gradient is deterministic for a
 // given grid. Registers hold the two row sets only (the column sums there would spill at 1024
 // lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
+// A persistent row kernel's workgroup number b, which picks its rows and its partial-sum row:
+// the dispatch index, or (PLAST_ROW_XCD) that index renumbered so that each XCD holds a
+// contiguous range of b.
+__device__ __forceinline__ uint32_t row_block() {
+  if constexpr (PLAST_ROW_XCD) return xcd_block(blockIdx.x, gridDim.x);
+  else return blockIdx.x;
+}
+
 // The rows a persistent row kernel's workgroup walks: r, r + S, ... below rend. Strided
 // (PLAST_ROW_BLOCKED 0): rows b, b + G, ..., so the grid sweeps the tensor front to back;
 // blocked (1): a contiguous block of ceil(N / G) rows per workgroup.
 __device__ __forceinline__ void row_range(uint32_t N, uint32_t G, uint32_t &r, uint32_t &S,
                                           uint32_t &rend) {
+  const uint32_t b = row_block();
   if constexpr (PLAST_ROW_BLOCKED) {
     const uint32_t per = (N + G - 1) / G;
-    r = blockIdx.x * per;
+    r = b * per;
     rend = r + per < N ? r + per : N;
     S = 1;
   } else {
-    r = blockIdx.x;
+    r = b;
     rend = N;
     S = G;
   }
@@ -697,7 +706,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     process(r + S, xb, yb, gb);
     load_row(r + 3 * S, xb, yb, gb);
   }
-  f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(blockIdx.x) * C);
+  f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(row_block()) * C);
 #pragma unroll
   for (int u = 0; u < V; ++u) {
     const uint32_t q = t + uint32_t(u) * BS;
