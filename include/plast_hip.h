@@ -146,7 +146,9 @@ typedef struct PlastFusedTape {
  * the reference CPU update in its operation order (src/optimizers/cpu/sgd.c:16-28,
  * adam.c:21-68, adamw.c:19-69); parameters that are NULL or have no grad are skipped; data and
  * grad are read as flat arrays of numel(param) floats, as the reference does. All parameters of one
- * call are updated by one kernel launch per group of up to 32 tensors.
+ * call are updated by one kernel launch. With more than 64 tensors their table is kept in device
+ * memory, and uploaded (waiting for the library stream) only when it differs from the previous
+ * call's; while a graph is captured such a call is recorded as one launch per 64 tensors.
  * Adam/AdamW: `t` is incremented first and the bias-corrected step
  * lr_t = lr * sqrt(1 - beta2^t) / (1 - beta1^t) is evaluated on the host exactly as the reference
  * evaluates it (double sqrt, float powf). On the first call, when optimizer->m is NULL, the moment

@@ -246,6 +246,8 @@ int num_cus();
 int library_device();
 // Called at the end of every entry point: checks the launch and, in synchronous mode, waits.
 void finish(const char *where);
+// True between plast_hip_capture_begin and plast_hip_capture_end (the stream records a graph).
+bool capturing();
 bool ensure_init();
 // Device scratch of at least `bytes`, owned by the library and reused across calls. Slot 0 holds
 // the reduction engine's partial summaries; slot 1 an op's own temporaries (tie counts, extremes);

@@ -1,13 +1,17 @@
 // optim.hip — optimizer updates (SGD, Adam, AdamW) and zero_grad over lists of parameter tensors.
 //
-// One launch updates up to kGroup tensors: the kernel argument block carries each tensor's
-// pointers and element count plus a prefix sum of its workgroup counts, so a workgroup finds its
-// tensor with a short uniform scan and then streams float4 units (a scalar loop covers a tensor's
-// last partial unit or an unaligned tensor). Per element the update is the reference CPU
+// One launch updates every tensor of a call: a table of entries (each tensor's pointers, element
+// count and first workgroup) tells a workgroup, by a uniform binary search, which tensor it
+// streams in float4 units (a scalar loop covers a tensor's last partial unit or an unaligned
+// tensor). Up to kGroup entries travel in the kernel argument block; a call with more keeps its
+// table in device memory, uploaded only when it differs from the last one (a training loop passes
+// the same parameters every step). While a graph is being captured, such a call is instead split
+// into launches of kGroup entries, so that no copy is recorded. Per element the update is the reference CPU
 // statement in its operation order (src/optimizers/cpu/{sgd.c:16-28, adam.c:62-66,
 // adamw.c:128-135}); the library is built without FMA contraction and sqrt/divide are correctly
 // rounded, so every element matches the CPU update bit for bit.
 #include <cmath>
+#include <cstring>
 #include <mutex>
 #include <unordered_set>
 #include <vector>
@@ -31,6 +35,23 @@ constexpr int kOptBlock = OPT == Opt::Sgd ? PLAST_SGD_BLOCK : PLAST_ADAM_BLOCK;
 template <Opt OPT>
 constexpr bool kOptXcd = (OPT == Opt::Sgd ? PLAST_SGD_XCD : PLAST_ADAM_XCD) != 0;
 
+struct OptScalars {
+  float lr;        // SGD: lr; Adam/AdamW: lr_t (bias-corrected)
+  float beta1, beta2, one_minus_beta1, one_minus_beta2, eps;
+  float decay;     // AdamW: lr * weight_decay
+};
+
+// One tensor (or one piece of a tensor longer than a launch's grid) of an update.
+struct OptEntry {
+  float *p;
+  const float *g;
+  float *m;
+  float *v;
+  uint64_t n;
+  uint32_t first_block;  // workgroups [first_block, next entry's first_block) update it
+  uint32_t vec;          // 1: every pointer is 16-byte aligned
+};
+
 struct OptArgs {
   float *p[kGroup];
   const float *g[kGroup];
@@ -40,13 +61,11 @@ struct OptArgs {
   uint32_t first_block[kGroup + 1];  // workgroups [first_block[i], first_block[i+1]) update tensor i
   uint32_t vec_mask;                 // bit i: tensor i's pointers are 16-byte aligned
   int count;
-  float lr;        // SGD: lr; Adam/AdamW: lr_t (bias-corrected)
-  float beta1, beta2, one_minus_beta1, one_minus_beta2, eps;
-  float decay;     // AdamW: lr * weight_decay
+  OptScalars s;
 };
 
 template <Opt OPT>
-__device__ __forceinline__ void update(const OptArgs &A, float &p, float g, float &m, float &v) {
+__device__ __forceinline__ void update(const OptScalars &A, float &p, float g, float &m, float &v) {
   if constexpr (OPT == Opt::Sgd) {
     p = p - A.lr * g;  // sgd.c:25
   } else {
@@ -71,30 +90,18 @@ __device__ __forceinline__ f4 ld(const float *p) {
   else return *reinterpret_cast<const f4 *>(p);
 }
 
-// XCD: XCD-contiguous workgroup numbering (used for launches holding one tensor entry).
-template <Opt OPT, bool XCD>
-__global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
+// The float4 units of one entry that workgroup `wb` (its number within the entry) updates.
+template <Opt OPT>
+__device__ __forceinline__ void update_entry(const OptScalars &S, float *P, const float *G, float *M,
+                                             float *V, uint64_t n, bool vec, uint32_t wb) {
   constexpr bool kMoments = OPT != Opt::Sgd;
   constexpr int kBs = kOptBlock<OPT>;
-  const uint32_t b = XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
-  // the last entry whose first workgroup is at or before b (uniform binary search)
-  int i = 0, hi = A.count - 1;
-  while (i < hi) {
-    const int mid = (i + hi + 1) >> 1;
-    if (A.first_block[mid] <= b) i = mid;
-    else hi = mid - 1;
-  }
-  const uint64_t n = A.n[i];
-  float *P = A.p[i];
-  const float *G = A.g[i];
-  float *M = kMoments ? A.m[i] : nullptr;
-  float *V = kMoments ? A.v[i] : nullptr;
-  const uint64_t unit0 = uint64_t(b - A.first_block[i]) * (kBs * kOptUnroll) + threadIdx.x;
+  const uint64_t unit0 = uint64_t(wb) * (kBs * kOptUnroll) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < kOptUnroll; ++u) {
     const uint64_t e = (unit0 + uint64_t(u) * kBs) * 4;
     if (e >= n) continue;
-    if (e + 4 <= n && (A.vec_mask >> i & 1u)) {
+    if (e + 4 <= n && vec) {
       f4 p = ld<kOptNtLoad<OPT>>(P + e);
       const f4 g = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(G + e));
       f4 m = f4(0.0f), v = f4(0.0f);
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         float pc = p[c], mc = m[c], vc = v[c];
-        update<OPT>(A, pc, g[c], mc, vc);
+        update<OPT>(S, pc, g[c], mc, vc);
         p[c] = pc;
         m[c] = mc;
         v[c] = vc;
@@ -123,7 +130,7 @@ __global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
           m = M[j];
           v = V[j];
         }
-        update<OPT>(A, p, G[j], m, v);
+        update<OPT>(S, p, G[j], m, v);
         P[j] = p;
         if constexpr (kMoments) {
           M[j] = m;
@@ -134,25 +141,94 @@ __global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
   }
 }
 
+// Entries in the kernel argument block. XCD: XCD-contiguous workgroup numbering (used for
+// launches holding one tensor entry).
+template <Opt OPT, bool XCD>
+__global__ __launch_bounds__(kOptBlock<OPT>) void opt_kernel(OptArgs A) {
+  constexpr bool kMoments = OPT != Opt::Sgd;
+  const uint32_t b = XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  // the last entry whose first workgroup is at or before b (uniform binary search)
+  int i = 0, hi = A.count - 1;
+  while (i < hi) {
+    const int mid = (i + hi + 1) >> 1;
+    if (A.first_block[mid] <= b) i = mid;
+    else hi = mid - 1;
+  }
+  update_entry<OPT>(A.s, A.p[i], A.g[i], kMoments ? A.m[i] : nullptr, kMoments ? A.v[i] : nullptr,
+                    A.n[i], (A.vec_mask >> i & 1u) != 0, b - A.first_block[i]);
+}
+
+// Entries in device memory (a call with more than kGroup of them).
+template <Opt OPT>
+__global__ __launch_bounds__(kOptBlock<OPT>) void opt_table_kernel(OptScalars S,
+                                                                   const OptEntry *__restrict__ T,
+                                                                   int count) {
+  constexpr bool kMoments = OPT != Opt::Sgd;
+  const uint32_t b = blockIdx.x;
+  int i = 0, hi = count - 1;
+  while (i < hi) {
+    const int mid = (i + hi + 1) >> 1;
+    if (T[mid].first_block <= b) i = mid;
+    else hi = mid - 1;
+  }
+  const OptEntry &E = T[i];
+  update_entry<OPT>(S, E.p, E.g, kMoments ? E.m : nullptr, kMoments ? E.v : nullptr, E.n,
+                    E.vec != 0, b - E.first_block);
+}
+
 bool f32_param(const Tensor *t) { return t && t->grad && t->dtype == FLOAT32 && t->grad->data && t->data; }
 
-// Launch OPT over parameters[0..count) in groups of kGroup tensors; m/v may be null for SGD.
+// The device copy of the last table of more than kGroup entries, and the host copy it was made
+// from (a call whose entries equal it launches without an upload).
+std::mutex g_table_mu;
+std::vector<OptEntry> g_table_host;
+OptEntry *g_table_dev = nullptr;
+size_t g_table_cap = 0;  // entries g_table_dev holds
+
+// The table in device memory, uploaded if it differs from the last one. The upload waits for the
+// library stream (earlier launches may still read the old table, and the host vector must outlive
+// the copy); it happens only when the parameter list changes.
+const OptEntry *device_table(const std::vector<OptEntry> &e, const char *where) {
+  if (e.size() == g_table_host.size() &&
+      memcmp(e.data(), g_table_host.data(), e.size() * sizeof(OptEntry)) == 0)
+    return g_table_dev;
+  g_table_host.clear();  // until the upload below succeeds
+  if (hipStreamSynchronize(stream()) != hipSuccess) {
+    report_error(where, "waiting for the library stream failed");
+    return nullptr;
+  }
+  if (e.size() > g_table_cap) {
+    if (g_table_dev) (void)hipFree(g_table_dev);
+    g_table_dev = nullptr;
+    g_table_cap = 0;
+    if (hipMalloc(&g_table_dev, e.size() * sizeof(OptEntry)) != hipSuccess) {
+      report_error(where, "allocation of the tensor table (%zu entries) failed", e.size());
+      g_table_dev = nullptr;
+      return nullptr;
+    }
+    g_table_cap = e.size();
+  }
+  if (hipMemcpyAsync(g_table_dev, e.data(), e.size() * sizeof(OptEntry), hipMemcpyHostToDevice,
+                     stream()) != hipSuccess ||
+      hipStreamSynchronize(stream()) != hipSuccess) {
+    report_error(where, "upload of the tensor table failed");
+    return nullptr;
+  }
+  g_table_host = e;
+  return g_table_dev;
+}
+
+// Launch OPT over parameters[0..count); m/v may be null for SGD. Every tensor's entries are
+// collected first: up to kGroup of them run from the kernel argument block, more from a device
+// table in one launch (or, during a graph capture, in launches of kGroup).
 template <Opt OPT>
 void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int count,
                     const char *where) {
   constexpr int kBs = kOptBlock<OPT>;
-  OptArgs A = base;
-  A.count = 0;
-  uint32_t blocks = 0;
-  auto flush = [&]() {
-    if (A.count == 0) return;
-    A.first_block[A.count] = blocks;
-    if (kOptXcd<OPT> && A.count == 1) opt_kernel<OPT, true><<<blocks, kBs, 0, stream()>>>(A);
-    else opt_kernel<OPT, false><<<blocks, kBs, 0, stream()>>>(A);
-    A.count = 0;
-    A.vec_mask = 0;
-    blocks = 0;
-  };
+  const uint64_t per_block = uint64_t(kBs) * kOptUnroll * 4;
+  // a tensor longer than one launch's grid allows is updated as several entries
+  const uint64_t max_piece = max_blocks(kBs) / 2 * per_block;
+  std::vector<OptEntry> entries;
   for (int k = 0; k < count; ++k) {
     Tensor *t = params[k];
     if (!t || !t->grad) continue;  // the reference skips these (sgd.c:20-22, adam.c:53-55)
@@ -167,24 +243,65 @@ void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int c
     float *V = v ? static_cast<float *>(v[k]->data) : nullptr;
     bool aligned = aligned16(P) && aligned16(G);
     if (m) aligned = aligned && aligned16(M) && aligned16(V);
-    // a tensor longer than one launch's grid allows is updated as several entries
-    const uint64_t per_block = uint64_t(kBs) * kOptUnroll * 4;
-    const uint64_t max_piece = max_blocks(kBs) / 2 * per_block;
     for (uint64_t off = 0; off < n; off += max_piece) {
       const uint64_t len = n - off < max_piece ? n - off : max_piece;
-      const uint64_t need = (len + per_block - 1) / per_block;
-      if (need > max_blocks(kBs) - blocks) flush();
-      const int i = A.count;
-      A.p[i] = P + off;
-      A.g[i] = G + off;
-      A.m[i] = M ? M + off : nullptr;
-      A.v[i] = V ? V + off : nullptr;
-      A.n[i] = len;
-      A.first_block[i] = blocks;
-      if (aligned) A.vec_mask |= 1u << i;
-      blocks += uint32_t(need);
-      if (++A.count == kGroup) flush();
+      OptEntry e;
+      e.p = P + off;
+      e.g = G + off;
+      e.m = M ? M + off : nullptr;
+      e.v = V ? V + off : nullptr;
+      e.n = len;
+      e.first_block = uint32_t((len + per_block - 1) / per_block);  // its workgroups, for now
+      e.vec = aligned ? 1u : 0u;
+      entries.push_back(e);
     }
+  }
+  if (entries.empty()) return;
+
+  // one launch from a device table: every workgroup number fits one grid
+  uint64_t total = 0;
+  for (const OptEntry &e : entries) total += e.first_block;
+  if (entries.size() > size_t(kGroup) && !capturing() && total <= max_blocks(kBs)) {
+    std::vector<OptEntry> table = entries;
+    uint32_t blocks = 0;
+    for (OptEntry &e : table) {
+      const uint32_t need = e.first_block;
+      e.first_block = blocks;
+      blocks += need;
+    }
+    std::lock_guard<std::mutex> lk(g_table_mu);
+    const OptEntry *T = device_table(table, where);
+    if (!T) return;
+    opt_table_kernel<OPT><<<blocks, kBs, 0, stream()>>>(base.s, T, int(table.size()));
+    return;
+  }
+
+  // launches of up to kGroup entries from the kernel argument block
+  OptArgs A = base;
+  A.count = 0;
+  uint32_t blocks = 0;
+  auto flush = [&]() {
+    if (A.count == 0) return;
+    A.first_block[A.count] = blocks;
+    if (kOptXcd<OPT> && A.count == 1) opt_kernel<OPT, true><<<blocks, kBs, 0, stream()>>>(A);
+    else opt_kernel<OPT, false><<<blocks, kBs, 0, stream()>>>(A);
+    A.count = 0;
+    A.vec_mask = 0;
+    blocks = 0;
+  };
+  for (const OptEntry &e : entries) {
+    const uint32_t need = e.first_block;
+    if (need > max_blocks(kBs) - blocks) flush();
+    const int i = A.count;
+    A.p[i] = e.p;
+    A.g[i] = e.g;
+    A.m[i] = e.m;
+    A.v[i] = e.v;
+    A.n[i] = e.n;
+    A.first_block[i] = blocks;
+    if (e.vec) A.vec_mask |= 1u << i;
+    blocks += need;
+    if (++A.count == kGroup) flush();
   }
   flush();
 }
@@ -285,13 +402,13 @@ void adam_like_step(OptT *o, Tensor **params, int count, const char *where) {
   }
   OptArgs A;
   memset(&A, 0, sizeof A);
-  A.lr = bias_corrected_lr(o->lr, o->beta1, o->beta2, o->t);
-  A.beta1 = o->beta1;
-  A.beta2 = o->beta2;
-  A.one_minus_beta1 = 1.0f - o->beta1;
-  A.one_minus_beta2 = 1.0f - o->beta2;
-  A.eps = o->epsilon;
-  if constexpr (OPT == Opt::AdamW) A.decay = o->lr * o->weight_decay;
+  A.s.lr = bias_corrected_lr(o->lr, o->beta1, o->beta2, o->t);
+  A.s.beta1 = o->beta1;
+  A.s.beta2 = o->beta2;
+  A.s.one_minus_beta1 = 1.0f - o->beta1;
+  A.s.one_minus_beta2 = 1.0f - o->beta2;
+  A.s.eps = o->epsilon;
+  if constexpr (OPT == Opt::AdamW) A.s.decay = o->lr * o->weight_decay;
   launch_updates<OPT>(A, params, o->m, o->v, count, where);
   finish(where);
 }
@@ -312,7 +429,7 @@ void sgd_step_hip(SGD *optimizer, Tensor **parameters, int num_parameters) {
   if (!ensure_init() || num_parameters <= 0 || !parameters) return;
   OptArgs A;
   memset(&A, 0, sizeof A);
-  A.lr = optimizer->lr;
+  A.s.lr = optimizer->lr;
   launch_updates<Opt::Sgd>(A, parameters, nullptr, nullptr, num_parameters, where);
   finish(where);
 }

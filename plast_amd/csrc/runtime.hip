@@ -56,6 +56,7 @@ hipStream_t stream() {
 }
 
 int num_cus() { return g_cus > 0 ? g_cus : 1; }
+bool capturing() { return g_capturing; }
 
 int library_device() { return g_device; }
 

@@ -1,7 +1,9 @@
 """GPU parity of the optimizer row: sgd/adam/adamw_step_hip and zero_grad_hip through the C-ABI,
 bit for bit against the oracle (itself pinned to the compiled reference and golden vectors) after
 three steps; parameters without gradients, NULL entries, misaligned tensors, more tensors than one
-launch group, and the moment allocation / release life cycle."""
+launch group (their table in device memory: two parameter lists in turn, so the table is replaced
+on every call, and a misaligned tensor inside it; under graph capture, launches of one group each,
+replayed against eager steps), and the moment allocation / release life cycle."""
 from __future__ import annotations
 
 import ctypes as C
@@ -157,3 +159,91 @@ def test_gpu_adam_caller_provided_moments_are_kept():
     want, mv, _ = run_host("oracle", "adam", [(300,)], 8, 1)
     assert_bits(p.numpy(), want[0], "adam with caller moments")
     assert_bits(m.numpy(), mv[0][0], "caller m")
+
+
+def _device_params(sizes, seed, misaligned=()):
+    """Device parameters with gradient buffers; positions in `misaligned` start 4 bytes into
+    their allocations. Returns (tensors kept alive, pointer array)."""
+    rt = _rt()
+    keep, ts = [], []
+    for i, x in enumerate(initial(sizes, seed)):
+        if i in misaligned:
+            n = x.size
+            base, gbase = rt.DeviceTensor((n + 1,)), rt.DeviceTensor((n + 1,))
+            p = rt.DeviceTensor(x.shape, base=base, offset=1, zero=False)
+            g = rt.DeviceTensor(x.shape, base=gbase, offset=1, zero=False)
+            p.t.grad = C.pointer(g.t)
+            _h2d(p.ptr, x)
+            keep += [base, gbase, p, g]
+            ts.append((p, g))
+        else:
+            d = rt.DeviceTensor.from_numpy(x, requires_grad=True)
+            keep.append(d)
+            ts.append((d, d.grad))
+    arr = (abi.TensorP * len(ts))(*[C.pointer(p.t) for p, _ in ts])
+    return ts, keep, arr
+
+
+@pytest.mark.parametrize("kind", ["sgd", "adamw"])
+def test_gpu_optimizer_tables_in_turn(kind):
+    """Two lists of more than one launch group (83 and 70 tensors, the second with a misaligned
+    tensor) stepped in turn: each call replaces the device table the other left."""
+    print(f"optimizer {kind}: two tables in turn", flush=True)
+    L = _rt().lib()
+    sizes_b = [(33,)] * 30 + [(1029,)] * 39 + [(7, 5)]
+    lists = [(OVER, 11, ()), (sizes_b, 12, (31,))]
+    state = []
+    for sizes, seed, mis in lists:
+        ts, keep, arr = _device_params(sizes, seed, mis)
+        state.append((sizes, seed, ts, keep, arr, make_opt(kind)))
+    step = getattr(L, f"{kind}_step_hip")
+    for s in range(3):
+        for sizes, seed, ts, keep, arr, opt in state:
+            for (p, g), gr in zip(ts, grads(sizes, seed, s)):
+                _h2d(g.ptr, gr)
+            step(C.byref(opt), C.cast(arr, abi.TensorPP), len(ts))
+            L.check(f"{kind}_step_hip")
+    for sizes, seed, ts, keep, arr, opt in state:
+        want, _, _ = run_host("oracle", kind, sizes, seed, 3, [True] * len(sizes))
+        for i, (p, _) in enumerate(ts):
+            assert_bits(p.numpy(), want[i], f"{kind} list of {len(sizes)}, p{i}")
+        if kind != "sgd":
+            getattr(L, f"plast_hip_{kind}_release")(C.byref(opt), len(ts))
+
+
+def test_gpu_optimizer_many_tensors_captured():
+    """An SGD step over 83 tensors captured as a graph (launches of one group each, no table
+    upload recorded) and replayed three times, eager work and synchronisations in between, equals
+    three eager steps bit for bit."""
+    print("optimizer: SGD over 83 tensors captured", flush=True)
+    L = _rt().lib()
+    results = []
+    for captured in (False, True):
+        ts, keep, arr = _device_params(OVER, 5)
+        for (p, g), gr in zip(ts, grads(OVER, 5, 0)):
+            _h2d(g.ptr, gr)
+        opt = make_opt("sgd")
+        ptrs = C.cast(arr, abi.TensorPP)
+        if not captured:
+            for _ in range(3):
+                L.sgd_step_hip(C.byref(opt), ptrs, len(ts))
+                L.check("sgd eager")
+        else:
+            assert L.plast_hip_capture_begin() == 0
+            try:
+                L.sgd_step_hip(C.byref(opt), ptrs, len(ts))
+            finally:
+                graph = L.plast_hip_capture_end()
+            L.check("capture")
+            assert graph
+            try:
+                for _ in range(3):
+                    assert L.plast_hip_graph_launch(graph) == 0
+                    L.plast_hip_synchronize()
+                    _rt().DeviceTensor((1000,)).fill_("uniform", 1, 0.0, 1.0)  # eager work
+            finally:
+                L.plast_hip_graph_destroy(graph)
+            L.check("replays")
+        results.append([p.numpy() for p, _ in ts])
+    for i, (e, c) in enumerate(zip(*results)):
+        assert_bits(c, e, f"captured SGD p{i}")
