@@ -271,7 +271,10 @@ def _call(kind: str, name: str, inputs, output, p: KernelParams):
     L = lib()
     n = len(inputs)
     arr = (_PTR_ARRAY[n] if n < len(_PTR_ARRAY) else TensorP * n)(*map(_ptr, inputs))
-    L.entry[kind, name](arr, _ptr(output), p)
+    fn = L.entry.get((kind, name))
+    if fn is None:
+        raise PlastHipError(f"no entry point {name}_hip_{kind}")
+    fn(arr, _ptr(output), p)
     if L.error_count():
         L.raise_error(f"{name}_hip_{kind}")
 
