@@ -265,7 +265,7 @@ class C1(Workload):
         else:
             forward(*self.call())
 
-    def c_us(self, calls: int = 20000, reps: int = 3):
+    def c_us(self, calls: int = 5000, reps: int = 3):
         """Wall microseconds per call when a C loop (bench_calls.c) makes the calls back to back,
         the library asynchronous and its stream drained at the end: what a C caller such as the
         reference's executor pays per call, without Python's cost. Best of `reps` loops; None for
