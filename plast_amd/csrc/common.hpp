@@ -90,7 +90,8 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_COL_SMALL_S4
 #define PLAST_COL_SMALL_S4 4
 #endif
-// Workgroups a leading-axis reduction is chunked up to. A row stream for whole contiguous rows
+// Workgroups a leading-axis reduction is chunked up to (512, 2048 and 4096 measured slower on every
+// leading-axis workload of the bench). A row stream for whole contiguous rows
 // of 2048-16384 columns (one 1024-lane workgroup per CU walking every G-th row, its column sums
 // in registers, then a finalize over the per-workgroup partials) was measured against this in one
 // process and removed: the [16384, 4096] bias gradient 5.40 against 5.62 TB/s, the one-pass
