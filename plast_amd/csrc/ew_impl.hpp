@@ -50,7 +50,8 @@ __device__ __forceinline__ f4 load4(const EwArgs<NIN> &A, int k, int64_t off) {
 // so each wave reads and writes whole contiguous 1 KiB runs per operand.
 template <class Body, bool REUSE>
 struct VecLaunch {
-  static constexpr int block = Body::kTape ? PLAST_TAPE_BLOCK : REUSE ? PLAST_EWR_BLOCK : PLAST_EW_BLOCK;
+  static constexpr int block = Body::kTape ? (REUSE ? PLAST_TAPE_REUSE_BLOCK : PLAST_TAPE_BLOCK)
+                                           : REUSE ? PLAST_EWR_BLOCK : PLAST_EW_BLOCK;
   static constexpr int unroll = Body::kTape ? PLAST_TAPE_UNROLL : REUSE ? PLAST_EWR_UNROLL : PLAST_EW_UNROLL;
   static constexpr bool xcd = (Body::kTape ? PLAST_TAPE_XCD : REUSE ? PLAST_EWR_XCD : PLAST_EW_XCD) != 0;
 };
