@@ -6,7 +6,8 @@ fixture: tests/conftest.py:56-58), its op sequence and its numpy closed form, an
 tests/test_ops.py:18-189, 205-287, 407-433 (elementwise, reductions, shape ops, leaky relu, ops with
 gradients) and tests/test_gradients.py:20-188 (autograd basics and per-op gradients), tests/test_edge_cases.py:6-147
 (small shapes, broadcasts, op chains, view ops) and tests/test_nn.py:35-110 (activations and losses
-composed of these ops: plast/nn/functional.py). Matmul, conv and Linear cases are out of this path. The expressions run through reference_api, which builds the DAG
+composed of these ops: plast/nn/functional.py) and tests/test_optim.py:22-112 (the optimizer steps
+whose gradients come from these ops). Matmul, conv and Linear cases are out of this path. The expressions run through reference_api, which builds the DAG
 of `<op>_hip_forward/backward` nodes."""
 from __future__ import annotations
 
@@ -425,3 +426,120 @@ def test_cross_entropy_loss(P, rng):
     rows, _ = ops.softmax_cross_entropy(rt.DeviceTensor.from_numpy(logits),
                                         rt.DeviceTensor.from_numpy(labels))
     close(np.array([rows.numpy().mean()]), loss.numpy(), rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------ test_optim.py: in-path cases
+# The reference's optimizer tests whose gradients come from this path's ops (its matmul-based
+# ones and the host-only learning-rate schedulers are off the path), stepped through
+# sgd/adam/adamw_step_hip and zero_grad_hip, each also checked against the update's closed form
+# (src/optimizers/cpu/sgd.c:25, adam.c:48-49, 63-65, adamw.c:130).
+def _step(kind, opt, params):
+    import ctypes as C
+    from plast_amd import abi
+    from plast_amd.runtime import lib
+    L = lib()
+    ptrs, keep = abi.tensor_array(*[p.dev.t for p in params])
+    getattr(L, f"{kind}_step_hip")(C.byref(opt), ptrs, len(params))
+    L.check(f"{kind}_step_hip")
+
+
+def _release(kind, opt, n):
+    import ctypes as C
+    from plast_amd.runtime import lib
+    getattr(lib(), f"plast_hip_{kind}_release")(C.byref(opt), n)
+
+
+def _adam_closed_form(p, grads, lr, b1, b2, eps, wd=0.0):
+    """The reference's update in float64, one gradient per step."""
+    p = p.astype(np.float64)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for t, g in enumerate(grads, start=1):
+        g = g.astype(np.float64)
+        p = p - lr * wd * p
+        m = b1 * m + (1 - b1) * g
+        v = b2 * v + (1 - b2) * g * g
+        lr_t = lr * np.sqrt(1 - b2 ** t) / (1 - b1 ** t)
+        p = p - lr_t * m / (np.sqrt(v) + eps)
+    return p
+
+
+def test_sgd_multiple_params(P, rng):
+    """test_optim.py:36-54: (w1 * x * w2).sum(), one SGD step over both parameters."""
+    from plast_amd import abi
+    w1n, w2n, xn = (rng.randn(3).astype(np.float32) for _ in range(3))
+    w1, w2, x = P.tensor(w1n, True), P.tensor(w2n, True), P.tensor(xn)
+    y = (w1 * x * w2).sum()
+    P.forward(y)
+    y.backward()
+    g1, g2 = w1.grad.numpy().copy(), w2.grad.numpy().copy()
+    close(g1, xn * w2n)
+    close(g2, w1n * xn)
+    lr = 0.05
+    _step("sgd", abi.SGD(lr), [w1, w2])
+    close(w1.numpy(), w1n - lr * g1)
+    close(w2.numpy(), w2n - lr * g2)
+
+
+def test_sgd_zero_grad(P, rng):
+    """test_optim.py:22-34: gradients are zero after zero_grad (the reference's matmul loss
+    replaced by (w * x).sum())."""
+    import ctypes as C
+    from plast_amd.runtime import lib
+    w = P.tensor(rng.randn(2, 3).astype(np.float32), True)
+    x = P.tensor(rng.randn(2, 3).astype(np.float32))
+    y = (w * x).sum()
+    P.forward(y)
+    y.backward()
+    assert np.abs(w.grad.numpy()).max() > 0
+    lib().zero_grad_hip(C.byref(w.dev.t))
+    lib().check("zero_grad_hip")
+    assert np.all(w.grad.numpy() == 0)
+
+
+def test_adam_multiple_steps(P, rng):
+    """test_optim.py:70-84: five steps of zero_grad, (w * x).sum() with x = 1, backward, step;
+    every gradient is 1, so w follows the closed-form update."""
+    import ctypes as C
+    from plast_amd import abi
+    from plast_amd.runtime import lib
+    w0 = rng.randn(3).astype(np.float32)
+    w = P.tensor(w0, True)
+    x = P.tensor(np.ones(3, dtype=np.float32))
+    lr, b1, b2, eps = 0.01, 0.9, 0.999, 1e-8
+    opt = abi.Adam(lr, b1, b2, eps, 0, None, None, None, None)
+    try:
+        for _ in range(5):
+            lib().zero_grad_hip(C.byref(w.dev.t))
+            y = (w * x).sum()
+            P.forward(y)
+            y.backward()
+            close(w.grad.numpy(), np.ones(3, np.float32))
+            _step("adam", opt, [w])
+            P.reset()
+        assert w.grad is not None
+        close(w.numpy(), _adam_closed_form(w0, [np.ones(3)] * 5, lr, b1, b2, eps),
+              rtol=1e-5, atol=1e-6)
+    finally:
+        _release("adam", opt, 1)
+
+
+def test_adamw_weight_decay(P):
+    """test_optim.py:101-112: w = [2, 2], (w * w).sum() (the tensor used twice: gradient 2w),
+    one AdamW step with lr 0.1 and weight decay 0.1."""
+    from plast_amd import abi
+    w0 = np.array([2.0, 2.0], dtype=np.float32)
+    w = P.tensor(w0, True)
+    y = (w * w).sum()
+    P.forward(y)
+    y.backward()
+    close(w.grad.numpy(), 2 * w0)
+    lr, b1, b2, eps, wd = 0.1, 0.9, 0.999, 1e-8, 0.1
+    opt = abi.AdamW(lr, b1, b2, eps, wd, 0, None, None, None, None)
+    try:
+        _step("adamw", opt, [w])
+        got = w.numpy()
+        assert not np.allclose(got, w0)
+        close(got, _adam_closed_form(w0, [2 * w0], lr, b1, b2, eps, wd), rtol=1e-5, atol=1e-6)
+    finally:
+        _release("adamw", opt, 1)
