@@ -41,8 +41,11 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_EWR_XCD
 #define PLAST_EWR_XCD 0
 #endif
+// Tape launches streaming every operand once: workgroup size. Measured in one process on config 2's
+// chain (two calls): 256 lanes 6555 / 6699 GB/s, 512 6692 / 6801, 384 6650, 768 6661, 1024 6425,
+// 256 with the XCD numbering 6395.
 #ifndef PLAST_TAPE_BLOCK
-#define PLAST_TAPE_BLOCK 256
+#define PLAST_TAPE_BLOCK 512
 #endif
 #ifndef PLAST_TAPE_UNROLL
 #define PLAST_TAPE_UNROLL 2
