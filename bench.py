@@ -504,8 +504,13 @@ class Optim(Workload):
         elif self.kind == "adamw":
             self.opt = abi.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01, 0, None, None, None, None)
         if self.kind in ("adam", "adamw"):
-            self.step()  # first step allocates the moments (outside the timed region)
-            lib().plast_hip_synchronize()
+            # zero moments owned by the bench (the library uses caller-set m and v as given), so
+            # that builds timed against each other in one process update the same buffers
+            self.moments = [[DeviceTensor((n,)) for _ in range(self.count)] for _ in range(2)]
+            self._marr = [(abi.TensorP * self.count)(*[C.pointer(t.t) for t in ms])
+                          for ms in self.moments]
+            self.opt.m = C.cast(self._marr[0], abi.TensorPP)
+            self.opt.v = C.cast(self._marr[1], abi.TensorPP)
 
     def step(self):
         L = lib()
@@ -516,9 +521,7 @@ class Optim(Workload):
             getattr(L, f"{self.kind}_step_hip")(C.byref(self.opt), self.ptrs, self.count)
 
     def free(self):
-        if self.kind in ("adam", "adamw"):
-            getattr(lib(), f"plast_hip_{self.kind}_release")(C.byref(self.opt), self.count)
-        for t in self.params:
+        for t in self.params + [t for ms in getattr(self, "moments", []) for t in ms]:
             t.free()
 
 

@@ -126,7 +126,8 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 // Persistent row kernels: workgroup numbers renumbered so that each XCD holds a contiguous range
 // (1) or dispatch order (0). Measured in one process: softmax forward 5947 against 5920 GB/s, the
-// one-pass step unchanged (5759 / 5760).
+// one-pass step unchanged (5759 / 5760): neutral within the 1-1.3% that two copies of one build
+// differ by in such a comparison.
 #ifndef PLAST_ROW_XCD
 #define PLAST_ROW_XCD 1
 #endif
