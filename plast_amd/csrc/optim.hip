@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "opt_plan.hpp"
 
 namespace plast {
 namespace {
@@ -39,17 +40,6 @@ struct OptScalars {
   float lr;        // SGD: lr; Adam/AdamW: lr_t (bias-corrected)
   float beta1, beta2, one_minus_beta1, one_minus_beta2, eps;
   float decay;     // AdamW: lr * weight_decay
-};
-
-// One tensor (or one piece of a tensor longer than a launch's grid) of an update.
-struct OptEntry {
-  float *p;
-  const float *g;
-  float *m;
-  float *v;
-  uint64_t n;
-  uint32_t first_block;  // workgroups [first_block, next entry's first_block) update it
-  uint32_t vec;          // 1: every pointer is 16-byte aligned
 };
 
 struct OptArgs {
@@ -178,44 +168,36 @@ __global__ __launch_bounds__(kOptBlock<OPT>) void opt_table_kernel(OptScalars S,
 
 bool f32_param(const Tensor *t) { return t && t->grad && t->dtype == FLOAT32 && t->grad->data && t->data; }
 
-// The device copy of the last table of more than kGroup entries, and the host copy it was made
-// from (a call whose entries equal it launches without an upload).
+// The device copy of the last table of more than kGroup entries (see OptTableCache).
 std::mutex g_table_mu;
-std::vector<OptEntry> g_table_host;
-OptEntry *g_table_dev = nullptr;
-size_t g_table_cap = 0;  // entries g_table_dev holds
+OptTableCache g_table;
 
 // The table in device memory, uploaded if it differs from the last one. The upload waits for the
 // library stream (earlier launches may still read the old table, and the host vector must outlive
 // the copy); it happens only when the parameter list changes.
 const OptEntry *device_table(const std::vector<OptEntry> &e, const char *where) {
-  if (e.size() == g_table_host.size() &&
-      memcmp(e.data(), g_table_host.data(), e.size() * sizeof(OptEntry)) == 0)
-    return g_table_dev;
-  g_table_host.clear();  // until the upload below succeeds
-  if (hipStreamSynchronize(stream()) != hipSuccess) {
-    report_error(where, "waiting for the library stream failed");
-    return nullptr;
-  }
-  if (e.size() > g_table_cap) {
-    if (g_table_dev) (void)hipFree(g_table_dev);
-    g_table_dev = nullptr;
-    g_table_cap = 0;
-    if (hipMalloc(&g_table_dev, e.size() * sizeof(OptEntry)) != hipSuccess) {
-      report_error(where, "allocation of the tensor table (%zu entries) failed", e.size());
-      g_table_dev = nullptr;
-      return nullptr;
-    }
-    g_table_cap = e.size();
-  }
-  if (hipMemcpyAsync(g_table_dev, e.data(), e.size() * sizeof(OptEntry), hipMemcpyHostToDevice,
-                     stream()) != hipSuccess ||
-      hipStreamSynchronize(stream()) != hipSuccess) {
-    report_error(where, "upload of the tensor table failed");
-    return nullptr;
-  }
-  g_table_host = e;
-  return g_table_dev;
+  return g_table.get(
+      e,
+      [&]() {
+        if (hipStreamSynchronize(stream()) == hipSuccess) return true;
+        report_error(where, "waiting for the library stream failed");
+        return false;
+      },
+      [&](size_t n) -> OptEntry * {
+        OptEntry *p = nullptr;
+        if (hipMalloc(&p, n * sizeof(OptEntry)) == hipSuccess) return p;
+        report_error(where, "allocation of the tensor table (%zu entries) failed", n);
+        return nullptr;
+      },
+      [](OptEntry *p) { (void)hipFree(p); },
+      [&](OptEntry *dst, const std::vector<OptEntry> &src) {
+        if (hipMemcpyAsync(dst, src.data(), src.size() * sizeof(OptEntry),
+                           hipMemcpyHostToDevice, stream()) == hipSuccess &&
+            hipStreamSynchronize(stream()) == hipSuccess)
+          return true;
+        report_error(where, "upload of the tensor table failed");
+        return false;
+      });
 }
 
 // Launch OPT over parameters[0..count); m/v may be null for SGD. Every tensor's entries are
@@ -236,74 +218,49 @@ void launch_updates(OptArgs base, Tensor **params, Tensor **m, Tensor **v, int c
       report_error(where, "parameter %d is not a float32 tensor with a gradient buffer", k);
       continue;
     }
-    const uint64_t n = numel(t);
     float *P = static_cast<float *>(t->data);
     const float *G = static_cast<const float *>(t->grad->data);
     float *M = m ? static_cast<float *>(m[k]->data) : nullptr;
     float *V = v ? static_cast<float *>(v[k]->data) : nullptr;
     bool aligned = aligned16(P) && aligned16(G);
     if (m) aligned = aligned && aligned16(M) && aligned16(V);
-    for (uint64_t off = 0; off < n; off += max_piece) {
-      const uint64_t len = n - off < max_piece ? n - off : max_piece;
-      OptEntry e;
-      e.p = P + off;
-      e.g = G + off;
-      e.m = M ? M + off : nullptr;
-      e.v = V ? V + off : nullptr;
-      e.n = len;
-      e.first_block = uint32_t((len + per_block - 1) / per_block);  // its workgroups, for now
-      e.vec = aligned ? 1u : 0u;
-      entries.push_back(e);
-    }
+    add_tensor(entries, P, G, M, V, numel(t), aligned, per_block, max_piece);
   }
   if (entries.empty()) return;
 
   // one launch from a device table: every workgroup number fits one grid
-  uint64_t total = 0;
-  for (const OptEntry &e : entries) total += e.first_block;
+  const uint64_t total = total_blocks(entries);
   if (entries.size() > size_t(kGroup) && !capturing() && total <= max_blocks(kBs)) {
     std::vector<OptEntry> table = entries;
-    uint32_t blocks = 0;
-    for (OptEntry &e : table) {
-      const uint32_t need = e.first_block;
-      e.first_block = blocks;
-      blocks += need;
-    }
+    number_entries(table);
     std::lock_guard<std::mutex> lk(g_table_mu);
     const OptEntry *T = device_table(table, where);
     if (!T) return;
-    opt_table_kernel<OPT><<<blocks, kBs, 0, stream()>>>(base.s, T, int(table.size()));
+    opt_table_kernel<OPT><<<unsigned(total), kBs, 0, stream()>>>(base.s, T, int(table.size()));
     return;
   }
 
   // launches of up to kGroup entries from the kernel argument block
-  OptArgs A = base;
-  A.count = 0;
-  uint32_t blocks = 0;
-  auto flush = [&]() {
-    if (A.count == 0) return;
-    A.first_block[A.count] = blocks;
-    if (kOptXcd<OPT> && A.count == 1) opt_kernel<OPT, true><<<blocks, kBs, 0, stream()>>>(A);
-    else opt_kernel<OPT, false><<<blocks, kBs, 0, stream()>>>(A);
-    A.count = 0;
+  for (const OptLaunch &g : group_entries(entries, size_t(kGroup), max_blocks(kBs))) {
+    OptArgs A = base;
+    A.count = int(g.count);
     A.vec_mask = 0;
-    blocks = 0;
-  };
-  for (const OptEntry &e : entries) {
-    const uint32_t need = e.first_block;
-    if (need > max_blocks(kBs) - blocks) flush();
-    const int i = A.count;
-    A.p[i] = e.p;
-    A.g[i] = e.g;
-    A.m[i] = e.m;
-    A.v[i] = e.v;
-    A.n[i] = e.n;
-    A.first_block[i] = blocks;
-    if (e.vec) A.vec_mask |= 1u << i;
-    blocks += need;
-    if (++A.count == kGroup) flush();
+    uint32_t blocks = 0;
+    for (size_t j = 0; j < g.count; ++j) {
+      const OptEntry &e = entries[g.first + j];
+      A.p[j] = e.p;
+      A.g[j] = e.g;
+      A.m[j] = e.m;
+      A.v[j] = e.v;
+      A.n[j] = e.n;
+      A.first_block[j] = blocks;
+      if (e.vec) A.vec_mask |= 1u << j;
+      blocks += e.first_block;
+    }
+    A.first_block[g.count] = blocks;
+    if (kOptXcd<OPT> && g.count == 1) opt_kernel<OPT, true><<<blocks, kBs, 0, stream()>>>(A);
+    else opt_kernel<OPT, false><<<blocks, kBs, 0, stream()>>>(A);
   }
-  flush();
 }
 
 // Moment arrays this library allocated (freed by the release calls).
