@@ -87,9 +87,11 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // Leading-axis finalize: lanes per output when there are at least twice as many chunks (1: one
 // lane, batches of 16 loads in sequence). Measured (two alternating runs): 8 lanes took config 1's
 // grad_b (16 chunks) from 9.4-9.9 to 7.3-7.5 us per call and the one-pass epilogue (64 chunks)
-// +3%, the [16384, 4096] bias gradient unchanged; 4 lanes lost 5% on that bias gradient.
+// +3%, the [16384, 4096] bias gradient unchanged; 4 lanes lost 5% on that bias gradient. In one
+// process (two calls, either order): 16 lanes took that bias gradient from 5603 / 5731 to
+// 5748 / 5864 GB/s and the one-pass epilogue +0.7-1.5%; 32 lanes land between.
 #ifndef PLAST_COL_FIN_Q
-#define PLAST_COL_FIN_Q 8
+#define PLAST_COL_FIN_Q 16
 #endif
 // Small leading-axis sums (at most PLAST_COL_SMALL_MAX input elements) in one launch: workgroups
 // of PLAST_COL_SMALL_S4 float4 columns that walk every row, instead of row chunks plus a finalize.
