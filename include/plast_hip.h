@@ -279,8 +279,10 @@ u32 plast_hip_fuse_elementwise_chains(DAG *dag, PlastArenaAllocFn alloc);
  * src/core/arena.c:20-24, 83-87, 98-102 and 108-127. Allocation failure prints and exits, as the
  * reference does (src/core/arena_cuda.cu:5-11). */
 void *arena_alloc_hip(u64 size);
-/* arena_free_hip during a graph capture (a garbage-collected tensor, say) is deferred: the buffer
- * is freed when the capture ends. */
+/* arena_free_hip during a graph capture (a garbage-collected tensor, say) is deferred: the captured
+ * kernels may use the buffer, so it is freed when the last graph the library made is destroyed
+ * (at once if the capture made no graph). A buffer freed outside a capture is freed at once: the
+ * caller keeps every buffer a live graph uses until that graph is destroyed. */
 void arena_free_hip(void *ptr);
 void arena_memset_hip(void *ptr, int value, u64 size);
 void arena_memcpy_h2d_hip(void *dest, const void *src, u64 size);

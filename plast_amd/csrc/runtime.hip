@@ -79,11 +79,11 @@ static void release_workspace(void *p) {
   (void)hipFree(p);
 }
 
-// Frees the buffers arena_free_hip was given during a capture (called once it has ended).
+// Hands the buffers arena_free_hip was given during a capture to the ledger once the capture has
+// ended: retired while a graph is alive (the capture's own graph may have been recorded using
+// them, and its replays keep those addresses), freed at once otherwise.
 static void release_deferred_frees() {
-  if (g_deferred_frees.empty()) return;
-  (void)hipStreamSynchronize(g_stream);
-  for (void *p : g_deferred_frees) (void)hipFree(p);
+  for (void *p : g_deferred_frees) g_ws.free_after_capture(p, release_workspace);
   g_deferred_frees.clear();
 }
 
@@ -340,8 +340,8 @@ void *plast_hip_capture_end(void) {
   g_capturing = false;
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(g_stream, &graph);
-  release_deferred_frees();
   if (e != hipSuccess || !graph) {
+    release_deferred_frees();
     report_error("plast_hip_capture_end", "%s", hipGetErrorString(e));
     return nullptr;
   }
@@ -349,10 +349,13 @@ void *plast_hip_capture_end(void) {
   e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   (void)hipGraphDestroy(graph);
   if (e != hipSuccess) {
+    release_deferred_frees();
     report_error("plast_hip_capture_end", "instantiate: %s", hipGetErrorString(e));
     return nullptr;
   }
   g_ws.graph_created(exec);
+  // buffers freed during the capture live as long as the graphs (this one included)
+  release_deferred_frees();
   return exec;
 }
 
@@ -448,7 +451,7 @@ void arena_free_hip(void *ptr) {
   if (!ptr || !ensure_init()) return;
   if (g_capturing) {
     // neither a wait nor hipFree may happen while the stream records (either would invalidate
-    // the capture): the buffer is freed when the capture ends
+    // the capture), and the captured kernels may use the buffer: it is freed with the last graph
     g_deferred_frees.push_back(ptr);
     return;
   }

@@ -490,6 +490,7 @@ constexpr int step_max_units() {
 }
 constexpr int kStepMaxV = step_max_units();
 constexpr uint64_t kStepMaxC = uint64_t(kStepBlock) * 4 * kStepMaxV;
+static_assert(kScratchFloats / kStepMaxC >= 256, "the device array holds a CU-sized grid of the widest rows");
 
 // Exact row statistics for the rare rows the fast path cannot take: the reference's serial max
 // fold, then the exp-sum with expf and the "some other term is non-finite" flag of the one-hot
@@ -813,6 +814,16 @@ int ce_step_form(const float *logits, const int32_t *labels, const float *dloss,
   if (C % 4 == 0 && C <= kStepMaxC && aligned16(logits) && aligned16(dlogits))
     return ce_step_units<1>(C);
   return 0;
+}
+
+// The one-pass step's workgroup count, shared by the allocating and the allocation-free entry
+// points so that both sum the bias gradient in the same order: one workgroup per row up to
+// PLAST_CE_STEP_WPC per CU, and no more than the allocation-free step's device array holds column
+// sums for (kScratchFloats / C; on MI355X, 256 CUs of rows up to 32768 floats, never binding).
+uint64_t ce_step_grid(uint64_t N, uint64_t C) {
+  uint64_t grid = uint64_t(num_cus()) * PLAST_CE_STEP_WPC;
+  if (grid > kScratchFloats / C) grid = kScratchFloats / C;
+  return N < grid ? N : grid;
 }
 
 // The one-pass step over `grid` workgroups with their column sums in part[grid][C], then their sum
@@ -1391,8 +1402,7 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
     if (dbias) bias_grad_reduce_hip(dlogits, dbias, N * C, C);
     return;
   }
-  const uint64_t grid = N < uint64_t(num_cus()) * PLAST_CE_STEP_WPC ? N
-                                                                     : uint64_t(num_cus()) * PLAST_CE_STEP_WPC;
+  const uint64_t grid = ce_step_grid(N, C);
   // the workgroups' column sums (written even when no bias gradient is wanted; then unread)
   float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
   if (!part) return;
@@ -1416,10 +1426,7 @@ void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *
   }
   float *part = noalloc_scratch(where);
   if (!part) return;
-  // the grid the scratch holds (every workgroup of a CU-sized grid, up to 32768 floats a row)
-  uint64_t grid = N < uint64_t(num_cus()) * PLAST_CE_STEP_WPC ? N
-                                                               : uint64_t(num_cus()) * PLAST_CE_STEP_WPC;
-  if (grid > kScratchFloats / C) grid = kScratchFloats / C;
+  const uint64_t grid = ce_step_grid(N, C);
   ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
   finish(where);
 }

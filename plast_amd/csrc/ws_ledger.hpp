@@ -5,6 +5,11 @@
 // were recorded with, so while any graph made by the library is alive an outgrown buffer is not
 // freed but retired; the retired buffers are freed when the last such graph is destroyed. With no
 // graph alive the old buffer is freed at once.
+//
+// Buffers the caller frees while a capture is open (arena_free_hip) are held back the same way:
+// the capture's own kernels may have been recorded reading or writing them, so once the capture
+// has produced a graph they are retired with the outgrown workspaces and freed with the last graph
+// (a capture that produced no graph frees them at once).
 #pragma once
 
 #include <algorithm>
@@ -43,6 +48,17 @@ class WorkspaceLedger {
   }
 
   void graph_created(const void *g) { graphs_.push_back(g); }
+
+  // A buffer freed while a capture was open, handed over when the capture ends: retired when a
+  // graph is alive (the capture's graph, just created, is), else released through release(ptr).
+  template <class Release>
+  void free_after_capture(void *p, Release release) {
+    if (!p) return;
+    if (graphs_.empty())
+      release(p);
+    else
+      retired_.push_back(p);
+  }
 
   // Forget graph `g` (false when the library did not make it); when it was the last one alive,
   // free the retired buffers through release(ptr).

@@ -66,6 +66,22 @@ int main() {
   CHECK(w.grow(0, 5000, 8192, fail, release) == nullptr && w.retired() == 1 && g_live.count(d));
   CHECK(w.graph_destroyed(&g3, release) && g_live.empty());
 
+  // buffers freed during a capture: released at once when the capture made no graph, retired with
+  // the graphs when it did (the graph may use them), and released with the last graph
+  void *f = alloc(32), *h = alloc(32), *k = alloc(32);
+  w.free_after_capture(f, release);  // no graph alive
+  CHECK(!g_live.count(f) && w.retired() == 0);
+  w.free_after_capture(nullptr, release);
+  w.graph_created(&g1);               // the capture's graph
+  w.free_after_capture(h, release);
+  CHECK(g_live.count(h) && w.retired() == 1);
+  w.graph_created(&g2);
+  w.free_after_capture(k, release);
+  CHECK(g_live.count(k) && w.retired() == 2);
+  CHECK(w.graph_destroyed(&g1, release) && g_live.count(h) && g_live.count(k));
+  CHECK(w.graph_destroyed(&g2, release) && !g_live.count(h) && !g_live.count(k));
+  CHECK(g_live.empty() && w.retired() == 0);
+
   std::printf(g_fail ? "FAILED\n" : "ok\n");
   return g_fail;
 }

@@ -7,8 +7,10 @@ stated tolerances:
   dlogits: 1e-5 of |value| + 1e-2 / N; dbias: 1e-5 of sum_rows |dlogits|.
 Rows hold NaN, -inf, zero maxima, signed zeros and huge spreads (the exact-refold path), labels
 sit in the SIMD tail of the loss's NEG rule, and shapes cover every register layout, rows that are
-not whole float4 (the three-pass path) and config 5's full [32768, 32000] (size-independent
-properties there: rows of dlogits sum to 0, the bias gradient's total mass is 0, the max matches)."""
+not whole float4 (the three-pass path), row counts several times the persistent grid (each
+workgroup loops over many rows, with special rows met in later iterations on both register sets)
+and config 5's full [32768, 32000] (sampled dlogits rows and every bias-gradient entry against a
+float64 closed form there)."""
 from __future__ import annotations
 
 import numpy as np
@@ -122,24 +124,139 @@ def test_step_is_deterministic_and_matches_the_op_path():
 
 
 def test_step_full_size_properties():
-    """Config 5 at [32768, 32000]: logits ~ N(0, 2), labels uniform. Sampled rows against a float64
-    log-sum-exp; every dlogits row sums to 0 (to 1e-5 / N per row); the bias gradient's total is 0;
-    the row max equals numpy's max."""
+    """Config 5 at [32768, 32000]: logits ~ N(0, 2), labels uniform, a per-row upstream gradient.
+    Against float64: the loss of sampled rows, 256 sampled rows of dlogits element by element
+    (g * (softmax - onehot) at 1e-5 of |value| + 1e-2 |g|), and every one of the 32000 bias-gradient
+    entries against the float64 column sums of that closed form over all 32768 rows (1e-5 of the
+    sum of the terms' magnitudes). Each workgroup walks 128 rows here. Size-independent properties
+    too: every dlogits row sums to 0, the row max equals numpy's."""
     from plast_amd import runtime as rt
     from plast_amd.abi import INT32
     N, Cn = 32768, 32000
     print("ce step full size", flush=True)
     X = rt.DeviceTensor((N, Cn), zero=False).fill_("normal", 42, 0.0, 2.0)
     Lb = rt.DeviceTensor((N,), INT32, zero=False).fill_("randint", 45, 0, Cn)
-    g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)
+    g = (np.random.RandomState(7).uniform(0.5, 1.5, N) / N).astype(np.float32)
     st, loss, dx, db = _step(rt, X, Lb, g)
     xh, yl = X.numpy(), Lb.numpy()
-    for r in np.random.RandomState(3).choice(N, 16, replace=False):
+    X.free()
+    rows = np.random.RandomState(3).choice(N, 256, replace=False)
+    for r in rows[:16]:
         row = xh[r].astype(np.float64)
         lse = np.log(np.exp(row - row.max()).sum()) + row.max()
         assert abs(loss[r] - (lse - row[yl[r]])) <= 1e-5 * (abs(lse) + abs(row[yl[r]]))
-        assert st[r, 0] == xh[r].max()
-    assert np.abs(dx.astype(np.float64).sum(1)).max() <= 1e-5 / N * 10
+    assert_bits(st[:, 0], xh.max(1), "row max")
+    print("ce step full size: float64 closed form", flush=True)
+    picked, col, acol = _closed_form_fp64(xh, yl, g, rows)
+    for r in rows:
+        assert_close_sum(dx[r], picked[r], np.abs(picked[r]) + 1e-2 * abs(float(g[r])), 1e-5,
+                         f"dlogits row {r}")
+    assert_close_sum(db, col, acol + 1e-12, 1e-5, "dbias against the float64 column sums")
+    assert np.abs(dx.astype(np.float64).sum(1)).max() <= 1e-5 * float(g.max()) * 10
     assert abs(db.astype(np.float64).sum()) <= 1e-4
-    assert_close_sum(db, dx.astype(np.float64).sum(0), np.abs(dx).astype(np.float64).sum(0) + 1e-12,
-                     1e-5, "dbias = column sums of dlogits")
+
+
+# Rows outnumber the one-pass step's workgroups (one per CU, 256 on MI355X) several times over, and
+# the row count is not a multiple of the grid: each workgroup's loop runs many iterations,
+# alternates its two register sets, ends on either set (odd and even row counts per workgroup) and
+# clamps its last prefetch to the final row. (771, 12000) gives each lane a ragged unit count.
+MANY_ROWS = [(805, 32000), (2085, 8192), (1281, 4096), (771, 12000)]
+GRID = 256
+
+
+def _late_special_rows(x, finite):
+    """Special rows placed where workgroup b meets them in its second, third and later iterations,
+    on both register sets (with a grid of G, row r is workgroup r % G's iteration r // G, held in
+    the first register set when that is even), and in the last two rows. `finite` keeps every
+    gradient finite (no NaN or all -inf row), so the bias gradient stays comparable."""
+    N, Cn = x.shape
+    G = GRID
+    at = [r for r in (G + 44, G + 45, 2 * G + 5, 2 * G + 6, 3 * G + 12, 3 * G + 13, 4 * G + 30,
+                      7 * G + 7, N - 2, N - 1) if 0 <= r < N]
+    kinds = ["zero_max", "overflow", "neg_inf_entry", "all_equal_huge"]
+    if not finite:
+        kinds += ["nan", "all_neg_inf"]
+    for i, r in enumerate(at):
+        k = kinds[i % len(kinds)]
+        if k == "zero_max":
+            x[r, :] = 0.0
+            x[r, 1::3] = -0.0
+        elif k == "overflow":
+            x[r, :] = -3.0e38
+            x[r, Cn // 3] = 3.0e38
+        elif k == "neg_inf_entry":
+            x[r, 7 % Cn] = -np.inf
+        elif k == "all_equal_huge":
+            x[r, :] = 1.0e30
+        elif k == "nan":
+            x[r, Cn - 1] = np.nan
+        elif k == "all_neg_inf":
+            x[r, :] = -np.inf
+    return at
+
+
+@pytest.mark.parametrize("specials", ["clean", "finite_specials", "nan_specials"])
+@pytest.mark.parametrize("N, Cn", MANY_ROWS, ids=[f"{n}x{c}" for n, c in MANY_ROWS])
+def test_step_many_rows_per_workgroup_matches_oracle(N, Cn, specials):
+    """Every row against the oracle with a per-row upstream gradient (zero and negative ones
+    included), at the bars of test_step_matches_oracle; the bias gradient against the float64
+    column sums of the oracle's dlogits wherever those are finite."""
+    from plast_amd import runtime as rt
+    print(f"ce step many rows {N}x{Cn} {specials}", flush=True)
+    rng = np.random.RandomState(N + 3 * Cn)
+    x = (rng.randn(N, Cn) * 2).astype(np.float32)
+    lab = rng.randint(0, Cn, N).astype(np.int32)
+    lab[N - 1] = Cn - 1                         # the label in the row's last float4
+    lab[N - 2] = 0
+    at = _late_special_rows(x, specials == "finite_specials") if specials != "clean" else []
+    if len(at) > 1:
+        lab[at[1]] = Cn // 3                    # the label on the overflowing row's maximum
+    g = (rng.uniform(0.2, 2.0, N) / N).astype(np.float32)
+    g[GRID + 44 if GRID + 44 < N else 0] = 0.0
+    g[2 * GRID + 5 if 2 * GRID + 5 < N else 1] = np.float32(-1.0 / N)
+    X, Lb = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab)
+    st, loss, dx, db = _step(rt, X, Lb, g)
+    wst, wloss, wdx = _oracle(x, lab, g)
+    assert_bits(st[:, 0], wst[:, 0], "row max")
+    assert_close_sum(st[:, 1], wst[:, 1], np.abs(wst[:, 1]) + 1e-6, 1e-5, "row log-sum-exp")
+    assert_close_sum(loss, wloss, np.abs(wloss) + np.abs(wst[:, 1]) + 1e-6, 1e-5, "row loss")
+    assert_bits(np.isnan(loss), np.isnan(wloss), "NaN rows of the loss")
+    finite = np.isfinite(wdx).all(1)
+    scale = np.abs(wdx[finite]) + np.abs(g[finite, None]) * 1e-2
+    assert_close_sum(dx[finite], wdx[finite], scale, 1e-5, "dlogits")
+    assert_bits(np.isnan(dx), np.isnan(wdx), "NaN positions of dlogits")
+    want = wdx.astype(np.float64).sum(0)
+    ok = np.isfinite(want)
+    if specials != "nan_specials":
+        assert ok.all(), "these inputs keep every column of the bias gradient finite"
+    assert_close_sum(db[ok], want[ok], np.abs(wdx.astype(np.float64)).sum(0)[ok] + 1e-12, 1e-5,
+                     "dbias")
+    assert_bits(np.isnan(db), np.isnan(want), "NaN columns of dbias")
+    # the same inputs again: identical bits (the column sums start from zero on every call)
+    st2, loss2, dx2, db2 = _step(rt, X, Lb, g)
+    for u, v, what in ((st2, st, "stats"), (loss2, loss, "loss"), (dx2, dx, "dlogits"),
+                       (db2, db, "dbias")):
+        assert_bits(u, v, f"repeat: {what}")
+
+
+def _closed_form_fp64(xh, yl, g, rows=None, chunk=1024):
+    """g_r * (softmax(x_r) - onehot(y_r)) in float64, for the listed rows, and its column sums
+    (and the sums of its magnitudes) over every row."""
+    N, Cn = xh.shape
+    col = np.zeros(Cn, np.float64)
+    acol = np.zeros(Cn, np.float64)
+    picked = {}
+    want_rows = set() if rows is None else set(int(r) for r in rows)
+    for r0 in range(0, N, chunk):
+        x64 = xh[r0:r0 + chunk].astype(np.float64)
+        x64 -= x64.max(1, keepdims=True)
+        np.exp(x64, out=x64)
+        x64 /= x64.sum(1, keepdims=True)
+        x64[np.arange(x64.shape[0]), yl[r0:r0 + chunk]] -= 1.0
+        x64 *= g[r0:r0 + chunk, None].astype(np.float64)
+        for r in want_rows.intersection(range(r0, r0 + x64.shape[0])):
+            picked[r] = x64[r - r0].copy()
+        col += x64.sum(0)
+        np.abs(x64, out=x64)
+        acol += x64.sum(0)
+    return picked, col, acol

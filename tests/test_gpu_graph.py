@@ -246,33 +246,43 @@ def test_workspace_outgrown_while_a_graph_lives():
 
 def test_free_during_capture_is_deferred():
     """A tensor freed while a graph is being recorded (Python may collect one at any time): the
-    free is deferred to the end of the capture instead of waiting on the recording stream, so the
-    capture stays valid and its replays match the eager op."""
+    free is deferred instead of waiting on the recording stream, so the capture stays valid. The
+    freed tensor here is the captured op's own input: its buffer is held until the graph is
+    destroyed, so every replay still reads it (the values it held, which the eager op gave), and
+    only the graph's destruction frees it."""
     rt = _rt()
     L = rt.lib()
-    print("graph: free during capture", flush=True)
+    print("graph: free of a captured input during capture", flush=True)
     x = rt.DeviceTensor((4096,), zero=False)
     y = rt.DeviceTensor((4096,), zero=False)
-    doomed = rt.DeviceTensor((1 << 20,), zero=False)
+    unused = rt.DeviceTensor((1 << 20,), zero=False)
     rng = np.random.RandomState(5)
     _h2d(x, rng.randn(4096))
     rt.forward("neg", [x], y)
+    want = y.numpy()
+    retired0, alive0 = L.plast_hip_workspace_retired(), L.plast_hip_graphs_alive()
     L.plast_hip_clear_error()
     assert L.plast_hip_capture_begin() == 0
     try:
         rt.forward("neg", [x], y)
-        doomed.free()                                   # deferred, not an error
+        x.free()                                        # the captured input: deferred
+        unused.free()                                   # a buffer the graph never touches
         assert L.plast_hip_error_count() == 0
     finally:
         graph = L.plast_hip_capture_end()
-    L.check("capture with a free inside")
+    L.check("capture with frees inside")
     assert graph
     try:
+        # both buffers are held with the graph's lifetime, not freed at the capture's end
+        assert L.plast_hip_workspace_retired() == retired0 + 2
+        scratch = rt.DeviceTensor((1 << 20,), zero=False).fill_("uniform", 9, -1.0, 1.0)
         for rep in range(3):
-            _h2d(x, rng.randn(4096))
+            _h2d(y, rng.randn(4096))
             assert L.plast_hip_graph_launch(graph) == 0
-            got = y.numpy()
-            rt.forward("neg", [x], y)
-            assert_bits(got, y.numpy(), f"replay {rep}")
+            assert_bits(y.numpy(), want, f"replay {rep} over the freed input")
+        scratch.free()
     finally:
         L.plast_hip_graph_destroy(graph)
+    assert L.plast_hip_graphs_alive() == alive0
+    if alive0 == 0:
+        assert L.plast_hip_workspace_retired() == 0

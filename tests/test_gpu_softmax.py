@@ -20,10 +20,26 @@ from plast_amd.abi import KernelParams
 
 pytestmark = pytest.mark.gpu
 
-# (600, 2052) and (300, 8192) give the persistent forward more rows than workgroups, the first with
-# a partial last float4 unit per lane
+# (600, 2052), (600, 2048) and (300, 8192) give the persistent forward more rows than workgroups
+# (with special rows in later iterations), the first with a partial last float4 unit per lane
 SHAPES = [(4, 10), (33, 1000), (8, 32000), (2, 3, 257), (1, 1), (5, 4096), (6, 9), (600, 2052),
-          (300, 8192)]
+          (600, 2048), (300, 8192)]
+
+
+def _put_specials(rows, r0):
+    rows[r0 + 0, 1] = np.nan                      # NaN row
+    rows[r0 + 1, :] = -np.inf                     # max is -FLT_MAX: every term 0, y NaN
+    rows[r0 + 2, 2] = np.inf                      # inf - inf
+    rows[r0 + 3, :2] = [3e38, -3e38]              # extreme spread: terms underflow
+    rows[r0 + 4, :] = 0.0                         # ties at zero, both signs
+    rows[r0 + 4, ::2] = -0.0
+    rows[r0 + 5, 0] = 1e-40                       # subnormal
+
+
+# The persistent forward runs one workgroup per CU (256 on MI355X) and holds two rows in turn
+# (iteration k of workgroup b is row k*256 + b, in the first register set when k is even): special
+# rows also sit in the second and third iterations, where the next row's loads are in flight.
+LATE_SPECIALS = (256 + 6, 512 + 8)
 
 
 def _x(shape, seed):
@@ -31,13 +47,10 @@ def _x(shape, seed):
     x = (rng.randn(*shape) * 3).astype(np.float32)
     rows = x.reshape(-1, shape[-1])
     if rows.shape[0] >= 6 and rows.shape[1] >= 4:
-        rows[0, 1] = np.nan                       # NaN row
-        rows[1, :] = -np.inf                      # max is -FLT_MAX: every term 0, y NaN
-        rows[2, 2] = np.inf                       # inf - inf
-        rows[3, :2] = [3e38, -3e38]               # extreme spread: terms underflow
-        rows[4, :] = 0.0                          # ties at zero, both signs
-        rows[4, ::2] = -0.0
-        rows[5, 0] = 1e-40                        # subnormal
+        _put_specials(rows, 0)
+        for r0 in LATE_SPECIALS:
+            if r0 + 6 <= rows.shape[0]:
+                _put_specials(rows, r0)
     return x
 
 

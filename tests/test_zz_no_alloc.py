@@ -1,8 +1,9 @@
 """The allocation-free cross-entropy step (softmax_cross_entropy_step_noalloc_hip) against the
 allocating one (softmax_cross_entropy_step_hip) through the C-ABI: stats, loss, dlogits and the
-bias gradient bit for bit (both run the same kernels over the same grid for rows up to 32768
-floats), on calls in a row whose second input is smaller than the first (the device array keeps the
-previous call's contents), and the rejection of rows the one-pass kernel cannot take."""
+bias gradient bit for bit (both run the same kernels over the same grid, one rule shared by the two
+entry points), on calls in a row whose second input is smaller than the first (the device array
+keeps the previous call's contents), with no workspace growth, recorded into a graph and replayed,
+and the rejection of rows the one-pass kernel cannot take."""
 from __future__ import annotations
 
 import numpy as np
@@ -47,6 +48,57 @@ def _same(rt, N, Cn, seed, special=False, with_bias=True):
     want = _run(rt, "softmax_cross_entropy_step_hip", X, Lb, G, with_bias)
     for name, a, b in zip(("stats", "loss", "dlogits", "dbias"), got, want):
         assert_bits(a, b, f"{N}x{Cn} {name}")
+
+
+def test_no_workspace_is_touched():
+    """The no-alloc calls leave every workspace slot's size as it was. In a fresh process every
+    slot is empty, so a call that went through the library's workspace for these column sums
+    (256 x 32768 floats) would grow slot 0; after other tests it would unless an earlier call had
+    already made the slot that large."""
+    from plast_amd import runtime as rt
+    L = rt.lib()
+    print("no-alloc step: workspace sizes", flush=True)
+    X, Lb, G = _inputs(rt, 300, 32768, 11)
+    before = [L.plast_hip_workspace_bytes(s) for s in range(3)]
+    a = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
+    b = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
+    assert [L.plast_hip_workspace_bytes(s) for s in range(3)] == before
+    for name, u, v in zip(("stats", "loss", "dlogits", "dbias"), a, b):
+        assert_bits(u, v, f"repeat {name}")
+
+
+def test_captured_no_alloc_step_replays():
+    """One no-alloc call recorded into a graph (after an eager call has looked up the device
+    array) and replayed with fresh logits between replays: each replay equals the eager call on the
+    same inputs, bit for bit."""
+    from plast_amd import runtime as rt
+    L = rt.lib()
+    print("no-alloc step: captured", flush=True)
+    N, Cn = 600, 4096
+    X, Lb, G = _inputs(rt, N, Cn, 12)
+    st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
+    dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
+    args = (X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr, db.ptr, N, Cn)
+    L.softmax_cross_entropy_step_noalloc_hip(*args)
+    L.check("eager no-alloc")
+    assert L.plast_hip_capture_begin() == 0
+    try:
+        L.softmax_cross_entropy_step_noalloc_hip(*args)
+    finally:
+        graph = L.plast_hip_capture_end()
+    L.check("capture of the no-alloc step")
+    assert graph
+    try:
+        for rep in range(3):
+            X.fill_("normal", 100 + rep, 0.0, 2.0)
+            assert L.plast_hip_graph_launch(graph) == 0
+            got = [t.numpy() for t in (st, loss, dx, db)]
+            L.softmax_cross_entropy_step_noalloc_hip(*args)
+            L.check("eager no-alloc")
+            for name, u, t in zip(("stats", "loss", "dlogits", "dbias"), got, (st, loss, dx, db)):
+                assert_bits(u, t.numpy(), f"replay {rep} {name}")
+    finally:
+        L.plast_hip_graph_destroy(graph)
 
 
 def test_two_calls_second_smaller():
