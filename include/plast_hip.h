@@ -194,10 +194,15 @@ void relu_grad_modulate_bias_grad_hip(const float *dout, const float *out_data, 
  * the gradient of a bias broadcast-added to the logits (the reference's ADD backward into a [C]
  * operand, kernel_macros.h:283-299). dloss [N] is the upstream gradient of each row's loss (1/N
  * for a mean), known before the step. Each logit is read once and each gradient written once
- * (16-byte aligned rows of whole float4 up to 32768 floats; other rows run the three passes). No counterpart in
- * the reference, which runs the op chain of src/api/loss.c:97-169, its backward and the bias's
- * ADD backward as separate passes; for callers that train with a cross-entropy loss. All pointers
- * are device memory; returns after the work completes (or is queued, in asynchronous mode). */
+ * (16-byte aligned rows of whole float4 up to 32768 floats; other rows run the three passes).
+ * stats, loss and dlogits are the same bits on every call; dbias, a sum over rows, is split over
+ * the GPU's workgroups by the rows each one took, which varies from call to call (its last bits
+ * may too) unless plast_hip_set_deterministic(1) fixes the split. No counterpart in the
+ * reference, which runs the op chain of src/api/loss.c:97-169, its backward and the bias's ADD
+ * backward as separate passes (its ADD backward accumulates the bias gradient with omp atomics,
+ * kernel_macros.h:292-297, in no fixed order either); for callers that train with a
+ * cross-entropy loss. All pointers are device memory; returns after the work completes (or is
+ * queued, in asynchronous mode). */
 void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, const float *dloss,
                                     float *stats, float *loss, float *dlogits, float *dbias, u64 N,
                                     u64 C);
@@ -208,10 +213,9 @@ void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, cons
  * routine, so it serves callers that cannot allocate: code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation. Only one-pass rows are taken: C a multiple of 4 up to
  * 32768, logits and dlogits 16-byte aligned, N below 2^31; anything else is reported as an error
- * (the three-pass form allocates). The results are bit-identical to
- * softmax_cross_entropy_step_hip's (the same kernels over the same grid). Calls that overlap on
- * one GPU (other streams, other threads) share the array and race. No counterpart in the
- * reference. */
+ * (the three-pass form allocates). The results are softmax_cross_entropy_step_hip's (the same
+ * kernels over the same grid; bit-identical in deterministic mode). Calls that overlap on one GPU
+ * (other streams, other threads) share the array and race. No counterpart in the reference. */
 void softmax_cross_entropy_step_noalloc_hip(const float *logits, const i32 *labels,
                                             const float *dloss, float *stats, float *loss,
                                             float *dlogits, float *dbias, u64 N, u64 C);
@@ -310,6 +314,13 @@ void transpose_backward_hip(float *da, const float *dout, const u64 *a_shape, co
 int plast_hip_init(int device);
 /* 1 (default): every entry point waits for its GPU work before returning. 0: asynchronous. */
 void plast_hip_set_sync(int sync);
+/* 1: results that are sums over many rows are the same bits on every call (the one-pass
+ * cross-entropy step's bias gradient: its rows are split over workgroups statically, about 10%
+ * slower on MI355X). 0 (default): workgroups take rows in order as they become free, so the
+ * split, and the last bits of such sums, vary between calls. No counterpart in the reference,
+ * whose CPU bias gradient accumulates with omp atomics (kernel_macros.h:292-297). */
+void plast_hip_set_deterministic(int on);
+int plast_hip_deterministic(void);
 /* Wait for all work queued on the library stream. Returns 0 on success. */
 int plast_hip_synchronize(void);
 /* Graph capture of launch-bound work. Between plast_hip_capture_begin() and

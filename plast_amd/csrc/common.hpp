@@ -133,6 +133,18 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_ROW_XCD
 #define PLAST_ROW_XCD 1
 #endif
+// Persistent row kernels: rows taken in pairs from a device counter (1) or the static strided
+// schedule (0; the one-pass step always uses it in deterministic mode). Measured with copies of
+// whole 128 KB rows by persistent 1024-lane workgroups on MI355X: 5.64-5.75 TB/s with the static
+// schedule (the odd XCDs finish about 8% after the even ones), 6.35-6.43 taking rows from a
+// counter, against 6.53 for the flat copy.
+#ifndef PLAST_ROW_DYNAMIC
+#define PLAST_ROW_DYNAMIC 1
+#endif
+// Persistent row kernels: a compiler barrier after each issue of row loads (1) or none (0).
+#ifndef PLAST_ROW_PIN
+#define PLAST_ROW_PIN 1
+#endif
 #ifndef PLAST_CE_STEP_NT_LOAD
 #define PLAST_CE_STEP_NT_LOAD 1  // the one-pass step's row loads: nontemporal (1) or ordinary (0)
 #endif
@@ -255,6 +267,8 @@ void report_error(const char *where, const char *fmt, ...) __attribute__((format
 hipStream_t stream();
 // Compute units of the library's device.
 int num_cus();
+// Whether results must be independent of timing (the one-pass step's row order is then static).
+bool deterministic();
 // The device the library runs on (its stream's), fixed at initialisation.
 int library_device();
 // Called at the end of every entry point: checks the launch and, in synchronous mode, waits.

@@ -14,6 +14,7 @@ int g_device = 0;
 bool g_inited = false;
 bool g_sync = true;
 bool g_capturing = false;  // the library stream is recording a graph
+bool g_deterministic = false;  // results must not depend on timing (plast_hip_set_deterministic)
 hipStream_t g_stream = nullptr;
 int g_err_count = 0;
 char g_err_msg[512] = "";
@@ -57,6 +58,7 @@ hipStream_t stream() {
 
 int num_cus() { return g_cus > 0 ? g_cus : 1; }
 bool capturing() { return g_capturing; }
+bool deterministic() { return g_deterministic; }
 
 int library_device() { return g_device; }
 
@@ -315,6 +317,8 @@ int plast_hip_init(int device) {
 }
 
 void plast_hip_set_sync(int sync) { g_sync = sync != 0; }
+void plast_hip_set_deterministic(int on) { g_deterministic = on != 0; }
+int plast_hip_deterministic(void) { return g_deterministic ? 1 : 0; }
 
 int plast_hip_capture_begin(void) {
   if (!ensure_init()) return -1;

@@ -473,11 +473,55 @@ __device__ __forceinline__ void row_range(uint32_t N, uint32_t G, uint32_t &r, u
   }
 }
 
+// Dynamic row order for the persistent row kernels. Workgroups take pairs of rows (2P, 2P + 1) in
+// increasing P from a device counter, so the rows in flight across the chip stay a compact band at
+// the front of the tensor and a workgroup that runs faster (on MI355X the odd XCDs stream about 8%
+// slower than the even ones under these loads) takes more rows; a static schedule of rows b, b + G,
+// ... leaves the fast XCDs idle at the end and spreads the band. One counter pair per kernel
+// family: [next pair, workgroups done]. The workgroup that finishes last returns both to zero for
+// the next launch (every earlier ticket has returned by then), so no reset is launched and a
+// captured graph replays it unchanged. Launches of one family overlapping on one device would
+// share the counter: the library issues them on its one stream.
+enum : int { kTicketStep = 0, kTicketSoftmax = 2 };
+static __device__ unsigned int g_row_tickets[4];
+
+// One ticket (a pair index), taken by lane 0 of wave 0; every other lane gets 0. The register is
+// set to 0 before the branch and the atomic returns into it, so nothing reads the atomic's result
+// where the branch rejoins: the wait for it falls where lane 0 first uses it. An increment
+// (global_atomic_inc, bounded by 2^32 - 1, so it never wraps here) rather than an add: the
+// compiler turns a uniform add into a wave-wide form whose result it reads, with a wait for every
+// outstanding load, right after the branch.
+__device__ __forceinline__ uint32_t take_ticket(int family) {
+  uint32_t v = 0;
+  if (threadIdx.x == 0) v = atomicInc(&g_row_tickets[family], 0xffffffffu);
+  return v;
+}
+
+// The end of a workgroup's ticket walk: `last` is its final ticket (its value makes lane 0 wait
+// for that atomic to return); the last workgroup out zeroes the family's counters.
+__device__ __forceinline__ void tickets_done(int family, uint32_t last) {
+  if (threadIdx.x != 0) return;
+  asm volatile("" ::"v"(last));
+  __threadfence();
+  if (atomicAdd(&g_row_tickets[family + 1], 1u) == gridDim.x - 1) {
+    __hip_atomic_store(&g_row_tickets[family], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_row_tickets[family + 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // A row unit of the persistent row kernels: nontemporal (NT) or ordinary load.
 template <bool NT>
 __device__ __forceinline__ f4 load_row_unit(const f4 *p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
   else return *p;
+}
+
+// Keeps the row loads just issued where they are. Without it the compiler may move a prefetch of
+// the next row down to where its values are first used (past the loop's back edge, behind the
+// wait for the current row), which shortens the registers' live ranges but leaves nothing in
+// flight while the current row is reduced. A compiler-only barrier: no instruction is emitted.
+__device__ __forceinline__ void pin_loads() {
+  if constexpr (PLAST_ROW_PIN) asm volatile("" ::: "memory");
 }
 
 constexpr int kStepBlock = PLAST_CE_STEP_BLOCK;
@@ -514,7 +558,7 @@ __device__ void ce_row_exact(const float *row, uint32_t C, int32_t y, float *lds
   bad = block_any<W>(b, lds);
 }
 
-template <int V>
+template <int V, bool DYN>
 __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     const float *__restrict__ x, const int32_t *__restrict__ lab, const float *__restrict__ dloss,
     float *__restrict__ stats, float *__restrict__ loss, float *__restrict__ dx,
@@ -523,6 +567,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // one area per reduction round of a row: a round's single barrier orders its writes after every
   // read of the same area in the previous row (which precede the other round's barrier)
   __shared__ float red1[2 * W], red2[W], ex[W + 2];
+  __shared__ uint32_t tk;  // the next pair, from lane 0 of wave 0 (dynamic order)
   extern __shared__ f4 colsum[];  // BS * V float4: the workgroup's column sums, then padding
   const uint32_t C4 = C / 4, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // row indices are 32-bit (the host checks N < 2^32): a 64-bit bound compare would be made in
@@ -560,6 +605,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
       const uint32_t off = (q < C4 ? q : C4 - 1) * 16u;
       v[u] = load_row_unit<PLAST_CE_STEP_NT_LOAD>(reinterpret_cast<const f4 *>(xr + off));
     }
+    pin_loads();
   };
 
   // One row held in v: v is overwritten with e = exp(x - M) by the sum pass, so the gradient
@@ -567,12 +613,16 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // e / S, within 2 ulp of it), with the one-hot term applied to the label's element alone. A
   // row's VALU work is then about 14 instructions per element, under the memory time (the
   // recomputed-exponential form took 36 and was issue-bound).
-  auto process = [&](uint32_t r, f4 (&v)[V], const int32_t y, const float g) {
+  // With `next`, lane 0 of wave 0 publishes `give` (a ticket) before the row's first barrier and
+  // every lane reads it into *next after it.
+  auto process = [&](uint32_t r, f4 (&v)[V], const int32_t y, const float g, uint32_t give,
+                     uint32_t *next) {
     // Consume every unit of the row here, on every path: a unit used only under a branch that some
     // waves skip (the row's ragged last unit) would leave its load pending past the loop's back
     // edge, and reusing its registers there would wait for every load, the prefetch included.
 #pragma unroll
     for (int u = 0; u < V; ++u) asm volatile("" ::"v"(v[u][0]), "v"(v[u][1]), "v"(v[u][2]), "v"(v[u][3]));
+    if (next && t == 0) tk = give;
     const uint32_t ti = lane_index();
     const uint32_t full = C4 / BS;  // units every lane holds inside the row
     // round 1: the row's max and min (lanes past the row hold a copy of its last float4, which
@@ -604,6 +654,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
           if (uint32_t(u) == yq / BS && c == int(y & 3)) xy = v[u][c];
     }
     __syncthreads();
+    if (next) *next = tk;
     float M = red1[0], MN = red1[W];
 #pragma unroll
     for (int w = 1; w < W; ++w) {
@@ -692,22 +743,49 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   // them), each reloaded right after its row is processed, so one row is always in flight and the
   // youngest memory operations at the loop's back edge are loads: the loop head may reuse a
   // register a store of the previous row still reads, and that wait then leaves the prefetch alone
-  // (with the stores last, it would wait for every load too).
-  uint32_t r, S, rend;
-  row_range(N, G, r, S, rend);
+  // (with the stores last, it would wait for every load too). Rows go in pairs, an odd last row
+  // after the loop: an exit between the pair's two rows would join the loop's back edge, and the
+  // waits at the loop head would then have to assume the first set's loads were the latest issued
+  // (waiting for the second set's prefetch too).
   f4 xa[V], xb[V];
   int32_t ya, yb;
   float ga, gb;
-  load_row(r, xa, ya, ga);
-  load_row(r + S, xb, yb, gb);
-  for (; r < rend; r += 2 * S) {
-    process(r, xa, ya, ga);
-    load_row(r + 2 * S, xa, ya, ga);
-    if (r + S >= rend) break;
-    process(r + S, xb, yb, gb);
-    load_row(r + 3 * S, xb, yb, gb);
+  if constexpr (DYN) {
+    // pairs of rows (2P, 2P + 1) from the ticket counter; the ticket for the pair after next is
+    // taken right before the first set's reload, so the wait for that reload covers it
+    if (t == 0) tk = take_ticket(kTicketStep);
+    __syncthreads();
+    uint32_t P = tk, Pn = 0;
+    uint32_t ahead = take_ticket(kTicketStep);
+    load_row(2 * P, xa, ya, ga);
+    load_row(2 * P + 1, xb, yb, gb);
+    while (2 * P + 1 < N) {
+      process(2 * P, xa, ya, ga, ahead, &Pn);
+      ahead = take_ticket(kTicketStep);
+      load_row(2 * Pn, xa, ya, ga);
+      process(2 * P + 1, xb, yb, gb, 0, nullptr);
+      load_row(2 * Pn + 1, xb, yb, gb);
+      P = Pn;
+    }
+    if (2 * P < N) process(2 * P, xa, ya, ga, 0, nullptr);
+    tickets_done(kTicketStep, ahead);
+  } else {
+    uint32_t r, S, rend;
+    row_range(N, G, r, S, rend);
+    load_row(r, xa, ya, ga);
+    load_row(r + S, xb, yb, gb);
+    for (; r + S < rend; r += 2 * S) {
+      process(r, xa, ya, ga, 0, nullptr);
+      load_row(r + 2 * S, xa, ya, ga);
+      process(r + S, xb, yb, gb, 0, nullptr);
+      load_row(r + 3 * S, xb, yb, gb);
+    }
+    if (r < rend) process(r, xa, ya, ga, 0, nullptr);
   }
-  f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(row_block()) * C);
+  // the workgroup's column sums: partial row b of part, in dispatch order under the dynamic
+  // order (the rows each workgroup took vary from run to run) and by the static schedule's
+  // numbering otherwise
+  f4 *p4 = reinterpret_cast<f4 *>(part + uint64_t(DYN ? blockIdx.x : row_block()) * C);
 #pragma unroll
   for (int u = 0; u < V; ++u) {
     const uint32_t q = t + uint32_t(u) * BS;
@@ -754,11 +832,12 @@ bool ce_step_lds_ok() {
   static bool granted = false;
   if (granted) return true;
   const int bytes = kStepBlock * V * int(sizeof(f4));
-  if (hipFuncSetAttribute(reinterpret_cast<const void *>(&ce_step_kernel<V>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
-    (void)hipGetLastError();  // not an error of the call: the caller takes the three passes
-    return false;
-  }
+  for (const void *k : {reinterpret_cast<const void *>(&ce_step_kernel<V, true>),
+                        reinterpret_cast<const void *>(&ce_step_kernel<V, false>)})
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+      (void)hipGetLastError();  // not an error of the call: the caller takes the three passes
+      return false;
+    }
   granted = true;
   return true;
 }
@@ -786,9 +865,13 @@ void ce_step_launch_v(int want, unsigned grid, float *part, const float *logits,
       return;
     }
     const size_t lds = size_t(kStepBlock) * V * sizeof(f4);
-    ce_step_kernel<V><<<grid, kStepBlock, lds, stream()>>>(logits, labels, dloss, stats, loss,
-                                                          dlogits, part, N, C,
-                                                          uint32_t(simd_end(N)));
+    // the dynamic row order unless results must not depend on timing (plast_hip_set_deterministic)
+    if (deterministic())
+      ce_step_kernel<V, false><<<grid, kStepBlock, lds, stream()>>>(
+          logits, labels, dloss, stats, loss, dlogits, part, N, C, uint32_t(simd_end(N)));
+    else
+      ce_step_kernel<V, true><<<grid, kStepBlock, lds, stream()>>>(
+          logits, labels, dloss, stats, loss, dlogits, part, N, C, uint32_t(simd_end(N)));
   }
 }
 
@@ -954,13 +1037,14 @@ __global__ __launch_bounds__(BS) void softmax_fwd_reg_kernel(const float *__rest
 // y = e * (1 / S) or (x - max) - log S. Without a NaN every x - max is <= 0 or -inf, where exp_le0
 // holds (about 1 ulp); a row with a NaN, whose fold may stop below some elements, takes expf and a
 // division.
-template <bool LOG, int V>
+template <bool LOG, int V, bool DYN>
 __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const float *__restrict__ x,
                                                                       float *__restrict__ y,
                                                                       uint32_t N, uint32_t C) {
   constexpr int BS = kStepBlock, W = BS / 64;
   // one area per reduction round (see ce_step_kernel)
   __shared__ float red1[2 * W], red2[W], ex[2];
+  __shared__ uint32_t tk;  // the next pair, from lane 0 of wave 0 (dynamic order)
   const uint32_t C4 = C / 4, t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint32_t G = gridDim.x;
   const float ninf = -__builtin_huge_valf();
@@ -978,10 +1062,14 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
       const uint32_t off = (q < C4 ? q : C4 - 1) * 16u;
       v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + off));
     }
+    pin_loads();
   };
-  auto process = [&](uint32_t r, f4 (&v)[V]) {
+  // process(r, v, give, next): with `next`, lane 0 of wave 0 publishes `give` (a ticket) before the
+  // row's first barrier and every lane reads it into *next after it
+  auto process = [&](uint32_t r, f4 (&v)[V], uint32_t give, uint32_t *next) {
 #pragma unroll
     for (int u = 0; u < V; ++u) asm volatile("" ::"v"(v[u][0]), "v"(v[u][1]), "v"(v[u][2]), "v"(v[u][3]));
+    if (next && t == 0) tk = give;
     const uint32_t ti = lane_index();
     const uint32_t full = C4 / BS;
     // round 1: the fast maximum and whether the row holds a NaN (lanes past the row hold a copy of
@@ -1002,6 +1090,7 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
       red1[W + wave] = nanw;
     }
     __syncthreads();
+    if (next) *next = tk;
     float M = red1[0], anynan = red1[W];
 #pragma unroll
     for (int w = 1; w < W; ++w) {
@@ -1074,17 +1163,39 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
       }
     }
   };
-  uint32_t r, S, rend;
-  row_range(N, G, r, S, rend);
   f4 xa[V], xb[V];
-  load_row(r, xa);
-  load_row(r + S, xb);
-  for (; r < rend; r += 2 * S) {
-    process(r, xa);
-    load_row(r + 2 * S, xa);
-    if (r + S >= rend) break;
-    process(r + S, xb);
-    load_row(r + 3 * S, xb);
+  if constexpr (DYN) {
+    // pairs of rows (2P, 2P + 1) from the ticket counter; the ticket for the pair after next is
+    // taken right before the first set's reload, so the wait for that reload covers it
+    if (t == 0) tk = take_ticket(kTicketSoftmax);
+    __syncthreads();
+    uint32_t P = tk, Pn = 0;
+    uint32_t ahead = take_ticket(kTicketSoftmax);
+    load_row(2 * P, xa);
+    load_row(2 * P + 1, xb);
+    while (2 * P + 1 < N) {
+      process(2 * P, xa, ahead, &Pn);
+      ahead = take_ticket(kTicketSoftmax);
+      load_row(2 * Pn, xa);
+      process(2 * P + 1, xb, 0, nullptr);
+      load_row(2 * Pn + 1, xb);
+      P = Pn;
+    }
+    if (2 * P < N) process(2 * P, xa, 0, nullptr);
+    tickets_done(kTicketSoftmax, ahead);
+  } else {
+    uint32_t r, S, rend;
+    row_range(N, G, r, S, rend);
+    load_row(r, xa);
+    load_row(r + S, xb);
+    // rows in pairs, an odd last row after the loop (see ce_step_kernel)
+    for (; r + S < rend; r += 2 * S) {
+      process(r, xa, 0, nullptr);
+      load_row(r + 2 * S, xa);
+      process(r + S, xb, 0, nullptr);
+      load_row(r + 3 * S, xb);
+    }
+    if (r < rend) process(r, xa, 0, nullptr);
   }
 }
 
@@ -1198,11 +1309,12 @@ void softmax_forward(const Tensor **inputs, Tensor *output, KernelParams params,
     const float *px = static_cast<const float *>(x->data);
     float *py = static_cast<float *>(output->data);
     const uint32_t n32 = uint32_t(N);
+    constexpr bool D = PLAST_ROW_DYNAMIC;
     switch (SV) {
-      case 1: softmax_fwd_step_kernel<LOG, 1><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
-      case 2: softmax_fwd_step_kernel<LOG, 2><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
-      case 4: softmax_fwd_step_kernel<LOG, 4><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
-      default: softmax_fwd_step_kernel<LOG, 8><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      case 1: softmax_fwd_step_kernel<LOG, 1, D><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      case 2: softmax_fwd_step_kernel<LOG, 2, D><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      case 4: softmax_fwd_step_kernel<LOG, 4, D><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
+      default: softmax_fwd_step_kernel<LOG, 8, D><<<G, kStepBlock, 0, stream()>>>(px, py, n32, C); break;
     }
     finish(where);
     return;

@@ -50,6 +50,8 @@ class Library:
         sig = {
             "plast_hip_init": ([C.c_int], C.c_int),
             "plast_hip_set_sync": ([C.c_int], None),
+            "plast_hip_set_deterministic": ([C.c_int], None),
+            "plast_hip_deterministic": ([], C.c_int),
             "plast_hip_synchronize": ([], C.c_int),
             "plast_hip_capture_begin": ([], C.c_int),
             "plast_hip_capture_end": ([], C.c_void_p),

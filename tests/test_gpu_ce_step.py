@@ -13,6 +13,8 @@ and config 5's full [32768, 32000] (sampled dlogits rows and every bias-gradient
 float64 closed form there)."""
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 import pytest
 
@@ -21,6 +23,20 @@ from hostlib import HostTensor, oracle_backward, oracle_forward
 from plast_amd.abi import KernelParams
 
 pytestmark = pytest.mark.gpu
+
+
+@contextlib.contextmanager
+def deterministic(on=True):
+    """plast_hip_set_deterministic for the duration (the step's bias gradient is then the same
+    bits on every call; by default its split over workgroups follows the run's timing)."""
+    from plast_amd import runtime as rt
+    L = rt.lib()
+    old = L.plast_hip_deterministic()
+    L.plast_hip_set_deterministic(int(on))
+    try:
+        yield
+    finally:
+        L.plast_hip_set_deterministic(old)
 
 
 def _step(rt, X, lab, g, with_bias=True):
@@ -98,8 +114,10 @@ def test_step_matches_oracle(N, Cn, special):
 
 
 def test_step_is_deterministic_and_matches_the_op_path():
-    """Two steps give identical bits; against the op path (forward op, overwriting backward op,
-    then the column sum) the row max is bit-equal and the rest within the bars above."""
+    """In deterministic mode two steps give identical bits; by default stats, loss and dlogits
+    still do and the bias gradient is within the sum bar of the deterministic one. Against the op
+    path (forward op, overwriting backward op, then the column sum) the row max is bit-equal and
+    the rest within the bars above."""
     from plast_amd import ops, runtime as rt
     N, Cn = 512, 32000
     print(f"ce step vs op path {N}x{Cn}", flush=True)
@@ -107,10 +125,16 @@ def test_step_is_deterministic_and_matches_the_op_path():
     from plast_amd.abi import INT32
     Lb = rt.DeviceTensor((N,), INT32, zero=False).fill_("randint", 45, 0, Cn)
     g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)
-    a = _step(rt, X, Lb, g)
-    b = _step(rt, X, Lb, g)
+    with deterministic():
+        a = _step(rt, X, Lb, g)
+        b = _step(rt, X, Lb, g)
     for u, v, what in zip(a, b, ("stats", "loss", "dlogits", "dbias")):
-        assert_bits(u, v, f"repeat: {what}")
+        assert_bits(u, v, f"deterministic repeat: {what}")
+    c = _step(rt, X, Lb, g)
+    for u, v, what in zip(a[:3], c[:3], ("stats", "loss", "dlogits")):
+        assert_bits(u, v, f"dynamic order: {what}")
+    assert_close_sum(c[3], a[3], np.abs(a[2]).astype(np.float64).sum(0) + 1e-12, 1e-5,
+                     "dynamic order: dbias")
     loss, stats = ops.softmax_cross_entropy(X, Lb, requires_grad=True)
     rt.lib().arena_memcpy_h2d_hip(loss.grad.ptr, g.ctypes.data, g.nbytes)
     rt.backward("softmax_cross_entropy", [X, Lb, stats], loss, KernelParams(0, 1, 0.0))
@@ -232,11 +256,24 @@ def test_step_many_rows_per_workgroup_matches_oracle(N, Cn, specials):
     assert_close_sum(db[ok], want[ok], np.abs(wdx.astype(np.float64)).sum(0)[ok] + 1e-12, 1e-5,
                      "dbias")
     assert_bits(np.isnan(db), np.isnan(want), "NaN columns of dbias")
-    # the same inputs again: identical bits (the column sums start from zero on every call)
+    # the same inputs again: identical per-row bits (the column sums start from zero on every
+    # call); then in deterministic mode, the static row split: the same bars, and its repeat is
+    # the same bits in every output
     st2, loss2, dx2, db2 = _step(rt, X, Lb, g)
-    for u, v, what in ((st2, st, "stats"), (loss2, loss, "loss"), (dx2, dx, "dlogits"),
-                       (db2, db, "dbias")):
+    for u, v, what in ((st2, st, "stats"), (loss2, loss, "loss"), (dx2, dx, "dlogits")):
         assert_bits(u, v, f"repeat: {what}")
+    assert_close_sum(db2[ok], want[ok], np.abs(wdx.astype(np.float64)).sum(0)[ok] + 1e-12, 1e-5,
+                     "dbias, second call")
+    with deterministic():
+        d1 = _step(rt, X, Lb, g)
+        d2 = _step(rt, X, Lb, g)
+    for u, v, what in zip(d1, d2, ("stats", "loss", "dlogits", "dbias")):
+        assert_bits(u, v, f"deterministic repeat: {what}")
+    for u, v, what in ((d1[0], st, "stats"), (d1[1], loss, "loss"), (d1[2], dx, "dlogits")):
+        assert_bits(u, v, f"deterministic against dynamic: {what}")
+    assert_close_sum(d1[3][ok], want[ok], np.abs(wdx.astype(np.float64)).sum(0)[ok] + 1e-12, 1e-5,
+                     "deterministic dbias")
+    assert_bits(np.isnan(d1[3]), np.isnan(want), "deterministic NaN columns of dbias")
 
 
 def _closed_form_fp64(xh, yl, g, rows=None, chunk=1024):

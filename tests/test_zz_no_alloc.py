@@ -1,17 +1,30 @@
 """The allocation-free cross-entropy step (softmax_cross_entropy_step_noalloc_hip) against the
 allocating one (softmax_cross_entropy_step_hip) through the C-ABI: stats, loss, dlogits and the
-bias gradient bit for bit (both run the same kernels over the same grid, one rule shared by the two
-entry points), on calls in a row whose second input is smaller than the first (the device array
+bias gradient bit for bit in deterministic mode (both run the same kernels over the same grid, one
+rule shared by the two entry points; by default the bias gradient's split over workgroups follows
+the run's timing, so there it is held to the sum bar), on calls in a row whose second input is smaller than the first (the device array
 keeps the previous call's contents), with no workspace growth, recorded into a graph and replayed,
 and the rejection of rows the one-pass kernel cannot take."""
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 import pytest
 
-from cases import assert_bits
+from cases import assert_bits, assert_close_sum
 
 pytestmark = pytest.mark.gpu
+
+
+@contextlib.contextmanager
+def deterministic(L, on=True):
+    old = L.plast_hip_deterministic()
+    L.plast_hip_set_deterministic(int(on))
+    try:
+        yield
+    finally:
+        L.plast_hip_set_deterministic(old)
 
 
 def _inputs(rt, N, Cn, seed, special=False):
@@ -43,11 +56,20 @@ def _run(rt, entry, X, Lb, G, with_bias=True):
 
 def _same(rt, N, Cn, seed, special=False, with_bias=True):
     print(f"no-alloc step {N}x{Cn} special={special} bias={with_bias}", flush=True)
+    L = rt.lib()
     X, Lb, G = _inputs(rt, N, Cn, seed, special)
-    got = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
-    want = _run(rt, "softmax_cross_entropy_step_hip", X, Lb, G, with_bias)
+    with deterministic(L):
+        got = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
+        want = _run(rt, "softmax_cross_entropy_step_hip", X, Lb, G, with_bias)
     for name, a, b in zip(("stats", "loss", "dlogits", "dbias"), got, want):
         assert_bits(a, b, f"{N}x{Cn} {name}")
+    # the default (dynamic) order: per-row outputs the same bits, the bias gradient to the sum bar
+    dyn = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
+    for name, a, b in zip(("stats", "loss", "dlogits"), dyn, want):
+        assert_bits(a, b, f"{N}x{Cn} {name}, dynamic order")
+    if with_bias:
+        assert_close_sum(dyn[3], want[3], np.abs(want[2]).astype(np.float64).sum(0) + 1e-12,
+                         1e-5, f"{N}x{Cn} dbias, dynamic order")
 
 
 def test_no_workspace_is_touched():
@@ -60,8 +82,9 @@ def test_no_workspace_is_touched():
     print("no-alloc step: workspace sizes", flush=True)
     X, Lb, G = _inputs(rt, 300, 32768, 11)
     before = [L.plast_hip_workspace_bytes(s) for s in range(3)]
-    a = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
-    b = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
+    with deterministic(L):
+        a = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
+        b = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
     assert [L.plast_hip_workspace_bytes(s) for s in range(3)] == before
     for name, u, v in zip(("stats", "loss", "dlogits", "dbias"), a, b):
         assert_bits(u, v, f"repeat {name}")
@@ -79,6 +102,14 @@ def test_captured_no_alloc_step_replays():
     st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
     dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
     args = (X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr, db.ptr, N, Cn)
+    with deterministic(L):
+        _captured_replays(L, args, X, st, loss, dx, db, exact=True)
+    # the default order: the counter its workgroups take rows from is returned to zero by every
+    # launch, so replays of a captured launch cover every row too
+    _captured_replays(L, args, X, st, loss, dx, db, exact=False)
+
+
+def _captured_replays(L, args, X, st, loss, dx, db, exact):
     L.softmax_cross_entropy_step_noalloc_hip(*args)
     L.check("eager no-alloc")
     assert L.plast_hip_capture_begin() == 0
@@ -95,8 +126,13 @@ def test_captured_no_alloc_step_replays():
             got = [t.numpy() for t in (st, loss, dx, db)]
             L.softmax_cross_entropy_step_noalloc_hip(*args)
             L.check("eager no-alloc")
-            for name, u, t in zip(("stats", "loss", "dlogits", "dbias"), got, (st, loss, dx, db)):
-                assert_bits(u, t.numpy(), f"replay {rep} {name}")
+            now = [t.numpy() for t in (st, loss, dx, db)]
+            for name, u, v in zip(("stats", "loss", "dlogits", "dbias"), got, now):
+                if exact or name != "dbias":
+                    assert_bits(u, v, f"replay {rep} {name}")
+                else:
+                    assert_close_sum(u, v, np.abs(now[2]).astype(np.float64).sum(0) + 1e-12,
+                                     1e-5, f"replay {rep} dbias")
     finally:
         L.plast_hip_graph_destroy(graph)
 
