@@ -17,6 +17,8 @@ ROOT = Path(__file__).resolve().parent.parent
 ORACLE_PATH = ROOT / "oracle" / "liboracle.so"
 REF_PATH = ROOT / "oracle" / "_ref" / "libplast_ref.so"
 NATIVE_PATH = ROOT / "oracle" / "_ref" / "libplast_ref_native.so"
+# the reference with the drop-in's scheduler edit applied, linked against the HIP library
+REF_HIP_PATH = ROOT / "oracle" / "_ref" / "libplast_ref_hip.so"
 
 _DT = {np.dtype(np.float32): FLOAT32, np.dtype(np.int32): INT32, np.dtype(np.int64): INT64}
 
