@@ -198,36 +198,60 @@ class C2Fused(Workload):
 class C1(Workload):
     """Config 1: Y = relu(X + b), X [1024,256], b [256] ~ U(-1,1); grad_b = sum_0 grad_Y. "big":
     the same fused chain over [16384, 4096] (a layer of realistic width, through the tape
-    interpreter's rows form)."""
+    interpreter's rows form). "dag" / "dagbig": the training step as the executor runs it - an
+    ADD and a LEAKY_RELU node with X and b requiring grad, fused by the elementwise-chain pass into
+    one node, then the graph's forward (Y) and backward (dX += 0 + dY * (Y > 0), grad_b += its
+    column sum, one pass) - at config 1's shape and at [16384, 4096]."""
 
     def __init__(self, part):
         self.part = part
         self.name = {"fwd": "config1_bias_relu_fwd_fused", "bwd": "config1_grad_b_sum_axis0",
                      "graph": "config1_step_fwd_bwd_graph",
-                     "big": "bias_relu_fused_16384x4096"}[part]
-        self.rows, self.cols = (16384, 4096) if part == "big" else (1024, 256)
+                     "big": "bias_relu_fused_16384x4096",
+                     "dag": "config1_step_dag_fused_fwd_bwd",
+                     "dagbig": "bias_relu_step_dag_16384x4096"}[part]
+        self.dag = part in ("dag", "dagbig")
+        self.rows, self.cols = (16384, 4096) if part in ("big", "dagbig") else (1024, 256)
         # calls of a few microseconds: enough of them that the timed region is not a handful of
         # host round trips
-        self.min_steps = 0 if part == "big" else 500
+        self.min_steps = 0 if part in ("big", "dagbig") else 500
         self.elems = self.rows * self.cols
-        fwd, bwd = self.elems * 8 + self.cols * 4, self.elems * 4 + self.cols * 4
-        self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd, "big": fwd}[part]
+        n, c = self.elems, self.cols
+        fwd, bwd = n * 8 + c * 4, n * 4 + c * 4
+        # the DAG's backward: dY and Y read, dX read and written, grad_b read and written
+        dag_bwd = n * 16 + c * 8
+        self.bytes_per_call = {"fwd": fwd, "bwd": bwd, "graph": fwd + bwd, "big": fwd,
+                               "dag": fwd + dag_bwd, "dagbig": fwd + dag_bwd}[part]
 
     def setup(self):
         R, Cn = self.rows, self.cols
-        self.X = DeviceTensor((R, Cn), zero=False).fill_("uniform", 42, -1.0, 1.0)
-        self.b = DeviceTensor((Cn,), zero=False).fill_("uniform", 43, -1.0, 1.0)
+        g = self.dag
+        self.X = DeviceTensor((R, Cn), requires_grad=g, zero=False).fill_("uniform", 42, -1.0, 1.0)
+        self.b = DeviceTensor((Cn,), requires_grad=g, zero=False).fill_("uniform", 43, -1.0, 1.0)
         self.gy = DeviceTensor((R, Cn), zero=False).fill_("uniform", 44, -1.0, 1.0)
-        self.Y = DeviceTensor((R, Cn), zero=False)
+        self.Y = DeviceTensor((R, Cn), requires_grad=g, zero=False)
         self.gb = DeviceTensor((Cn,), zero=False)
+        if self.dag:
+            self.S = DeviceTensor((R, Cn), requires_grad=True, zero=False)
+            self.Y.grad.fill_("uniform", 44, -1.0, 1.0)
         from plast_amd.ops import make_tape
         self.tape = make_tape([("LOAD", 0, 0, 0, 0.0), ("ADD", abi.SRC_INPUT, 1, 0, 0.0),
                                ("LEAKY_RELU", 0, 0, 0, 0.0)], 2)
 
         self.graph = None
+        self.g = None
         self.rebind()
 
     def rebind(self):
+        if self.dag:
+            # the executor's graph over this build's op slots, fused by this build's pass
+            self.g = Graph()
+            self.g.node("add", [self.X, self.b], self.S)
+            self.g.node("leaky_relu", [self.S], self.Y, KernelParams(0, 0, 0.0))
+            if self.g.build(self.Y, fuse=True) != 1 or self.g.op_types() != ["FUSED_ELEMENTWISE"]:
+                raise SystemExit(f"bench.py: the pass did not fuse config 1's step: "
+                                 f"{self.g.op_types()}")
+            return
         if self.part != "graph":
             return
         if self.graph:
@@ -259,7 +283,10 @@ class C1(Workload):
         return "sum", [self.gy], self.gb, KernelParams(0, 0, 0.0)
 
     def step(self):
-        if self.part == "graph":
+        if self.dag:
+            self.g.forward()
+            self.g.backward()
+        elif self.part == "graph":
             if lib().plast_hip_graph_launch(self.graph) != 0:
                 raise SystemExit("bench.py: graph launch failed")
         else:
@@ -296,7 +323,7 @@ class C1(Workload):
         """Device microseconds per call without the host's per-call cost: `calls` back-to-back
         calls captured as one graph, replayed `reps` times (the graph launch is spread over the
         calls). None for the graph workload itself."""
-        if self.part not in ("fwd", "bwd"):
+        if self.part not in ("fwd", "bwd", "dag"):
             return None
         import gc
         L = lib()
@@ -732,6 +759,7 @@ def detail_workloads():
     return {
         "copy": Copy(),
         "c1f": C1("fwd"), "c1b": C1("bwd"), "c1g": C1("graph"), "c1big": C1("big"),
+        "c1dag": C1("dag"), "c1dagbig": C1("dagbig"),
         "c2f": C2Fused(True), "c2u": C2Fused(False),
         "c3f": C3("fused"), "c3a": C3("add"), "c3m": C3("mul"),
         "c4sum": C4("sum", 1), "c4mean": C4("mean", 1), "c4max": C4("max", 1),
@@ -756,7 +784,7 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     gbs = w.bytes_per_call / (ms * 1e-3) / 1e9
     r = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
          "elems_per_s": round(w.elems / (ms * 1e-3), 1), "algorithmic_bytes": w.bytes_per_call}
-    if isinstance(w, C1) and w.part != "big":
+    if isinstance(w, C1) and w.part not in ("big", "dagbig"):
         # latency-bound: microseconds per call as a Python caller and a C caller see them, and on
         # the device alone
         r["us_per_call"] = round(ms * 1e3, 2)

@@ -76,7 +76,13 @@ PLAST_HIP_KERNEL_PAIR(transpose)
 
 /* Fused elementwise chain: no reference counterpart (the reference fuses only matmul/conv
  * epilogues: src/scheduler/fusion.c:28-90). params.dim holds a `const PlastFusedTape *` (host
- * memory); inputs are the chain's external tensors in tape order. One kernel launch. */
+ * memory); inputs are the chain's external tensors in tape order. One kernel launch. The forward
+ * writes only the chain's output. The backward is a no-op for a chain formed without gradients;
+ * the one chain formed with them, leaky_relu(x + bias, alpha >= 0) over row-major x and a bias row,
+ * adds 0 + dy * (y > 0 ? 1 : alpha) into x->grad (bit for bit the unfused nodes' backwards,
+ * unary_ops.c:236-258 then kernel_macros.h:283-299) and the same terms summed over rows into
+ * bias->grad (summation order: the library's, as the reference's omp atomics leave it open), in
+ * one launch when both require grad. */
 PLAST_HIP_KERNEL_PAIR(fused_elementwise)
 
 /* Softmax cross-entropy: no reference op; replaces the op chain of src/api/loss.c:97-169 up to NEG.
@@ -273,7 +279,11 @@ typedef void *(*PlastArenaAllocFn)(Arena *arena, u64 size, u64 align);
  * src/core/graph.c:52-55): every maximal run of GPU elementwise nodes in which each intermediate
  * tensor feeds only the next node, nothing in the run requires grad, and the chain has at most
  * PLAST_TAPE_MAX_INPUTS external inputs is replaced by one FUSED_ELEMENTWISE node writing the last
- * node's output, spliced into the node array the way fusion_apply does (fusion.c:155-206).
+ * node's output, spliced into the node array the way fusion_apply does (fusion.c:155-206). So is
+ * an ADD(x, bias) feeding only a LEAKY_RELU with alpha >= 0 when x or the bias requires grad
+ * (x row-major fp32 of the output's shape, the bias a row-major row of its last extent): the fused
+ * node's backward writes both gradients, and the intermediate x + bias (and its gradient) is
+ * never written.
  * Returns the number of chains fused. Called from fusion_optimize (fusion.c:209-224). */
 u32 plast_hip_fuse_elementwise_chains(DAG *dag, PlastArenaAllocFn alloc);
 

@@ -486,12 +486,7 @@ void fused_elementwise_hip_forward(const Tensor **inputs, Tensor *output, Kernel
   finish(where);
 }
 
-void fused_elementwise_hip_backward(Tensor **inputs, const Tensor *output, KernelParams params) {
-  (void)inputs;
-  (void)params;
-  // The fusion pass only forms chains in which nothing requires grad.
-  if (output->requires_grad)
-    report_error("fused_elementwise_hip_backward", "fused chains carry no gradient");
-}
+// fused_elementwise_hip_backward (the one chain that carries a gradient) is in epilogue.hip, beside
+// the bias-gradient kernels it shares.
 
 }  // extern "C"

@@ -169,6 +169,18 @@ struct ReluGradBody : ScalarBody<ReluGradBody> {
   }
 };
 
+// operands: dout, y, dx  ->  dx + (0 + dout * (y > 0 ? 1 : alpha)): x's gradient through a fused
+// leaky_relu(x + bias) node, the leaky backward into the intermediate's zeroed gradient
+// (unary_ops.c:236-258) then the ADD backward's accumulation (kernel_macros.h:283-299), with the
+// mask read from the node's output (the same for alpha >= 0)
+struct LeakyAddGradAccumBody : ScalarBody<LeakyAddGradAccumBody> {
+  static constexpr int NIN = 3;
+  float alpha;
+  __device__ __forceinline__ float eval(const float *v, uint64_t) const {
+    return v[2] + (0.0f + v[0] * (v[1] > 0.0f ? 1.0f : alpha));
+  }
+};
+
 // operands: da, g  ->  da + g  (reshape backward, sum backward broadcast, transpose backward)
 struct AccumBody : ScalarBody<AccumBody> {
   static constexpr int NIN = 2;

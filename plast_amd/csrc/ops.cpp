@@ -3,6 +3,7 @@
 #include <vector>
 
 #include "../../include/plast_hip.h"
+#include "fused_grad.hpp"
 
 namespace {
 
@@ -84,7 +85,7 @@ bool same_shape(const Tensor *a, const Tensor *b) {
 }
 
 // A node the pass may place in a chain: a GPU fp32 elementwise op with nothing requiring grad
-// (fused chains have no backward).
+// (the only fused chain with a backward is the leaky_relu(x + bias) pair below).
 bool fusable(const Node *n) {
   if (!is_binary(n->op_type) && !is_unary(n->op_type)) return false;
   if (n->num_inputs != (is_binary(n->op_type) ? 2 : 1)) return false;
@@ -94,6 +95,14 @@ bool fusable(const Node *n) {
     const Tensor *t = n->inputs[i];
     if (!t || t->device != GPU || t->dtype != FLOAT32 || t->requires_grad) return false;
   }
+  return true;
+}
+
+// A member of the fused leaky_relu(x + bias) pair: fp32 GPU tensors, gradients allowed.
+bool grad_pair_member(const Node *n) {
+  if (!plast::fused_grad::gpu_f32(n->output)) return false;
+  for (int i = 0; i < n->num_inputs; ++i)
+    if (!plast::fused_grad::gpu_f32(n->inputs[i])) return false;
   return true;
 }
 
@@ -180,6 +189,31 @@ u32 plast_hip_fuse_elementwise_chains(DAG *dag, PlastArenaAllocFn alloc) {
 
   std::vector<bool> taken(n, false);
   std::vector<Chain> chains;
+  // leaky_relu(x + bias, alpha >= 0) with gradients: its backward reads the mask from the output,
+  // so the intermediate x + bias must feed the leaky node alone (it is never written)
+  for (u32 i = 0; i < n; ++i) {
+    const Node *a = nodes[i];
+    if (a->op_type != ADD || a->num_inputs != 2 || !grad_pair_member(a)) continue;
+    const Tensor *t = a->output;
+    if (t == root_out) continue;
+    const u32 l = consumer(t, i + 1);
+    if (l >= n || nodes[l]->op_type != LEAKY_RELU || nodes[l]->num_inputs != 1 ||
+        !grad_pair_member(nodes[l]) || uses(t) != 1)
+      continue;
+    const Tensor *y = nodes[l]->output;
+    if (!plast::fused_grad::alpha_ok(nodes[l]->params.fval) || !plast::fused_grad::same_extents(t, y) ||
+        plast::fused_grad::x_operand(a->inputs[0], a->inputs[1], y) < 0)
+      continue;
+    const bool grads = a->inputs[0]->requires_grad || a->inputs[1]->requires_grad;
+    if (!grads) continue;  // no gradients: the chain loop below takes it (and may extend it)
+    Chain c;
+    memset(&c.tape, 0, sizeof c.tape);
+    if (!append(c, a, nullptr) || !append(c, nodes[l], t)) continue;
+    c.idx = {i, l};
+    c.tape.num_inputs = u32(c.ext.size());
+    taken[i] = taken[l] = true;
+    chains.push_back(c);
+  }
   for (u32 i = 0; i < n; ++i) {
     if (taken[i] || !fusable(nodes[i])) continue;
     Chain c;

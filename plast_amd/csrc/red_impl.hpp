@@ -61,6 +61,45 @@ struct ReluGradStore {
   }
 };
 
+// The gradient a fused leaky_relu(x + bias) node hands to its ADD, for the operands (dout, y):
+// 0 + dout * (y > 0 ? 1 : alpha), the chain's leaky backward (unary_ops.c:236-258) accumulated into
+// the intermediate's zeroed gradient, with its mask read from the node's output y (for alpha >= 0,
+// y > 0 exactly where x + bias > 0). Summed over rows: the bias's gradient.
+struct LeakyAddGrad {
+  static constexpr int NIN = 2;
+  float alpha;
+  __device__ __forceinline__ float eval(const float *v) const {
+    return 0.0f + v[0] * (v[1] > 0.0f ? 1.0f : alpha);
+  }
+};
+
+// The same term for the operands (dout, y, g), summed, with g + term stored to dst (g's own
+// buffer): x's gradient from the ADD's backward (kernel_macros.h:283-299) written in the pass that
+// sums the bias's. A refold recomputes its terms from dout and y, which the stores leave intact.
+struct LeakyAddGradStore {
+  static constexpr int NIN = 3;
+  static constexpr bool kStore = true;
+  static constexpr bool kRefoldInputs = true;
+  float alpha;
+  float *dst;
+  __device__ __forceinline__ float eval(const float *v) const {
+    return 0.0f + v[0] * (v[1] > 0.0f ? 1.0f : alpha);
+  }
+  __device__ __forceinline__ float stored(const float *v, float y) const { return v[2] + y; }
+};
+
+// What a storing producer writes for the value y it sums at operands v: y itself, or, for one
+// with kRefoldInputs, its own stored(v, y).
+template <class P, class = void>
+struct StoresOther : std::false_type {};
+template <class P>
+struct StoresOther<P, std::void_t<decltype(P::kRefoldInputs)>> : std::bool_constant<P::kRefoldInputs> {};
+template <class P>
+__device__ __forceinline__ float stored_value(const P &prod, const float *v, float y) {
+  if constexpr (StoresOther<P>::value) return prod.stored(v, y);
+  else return y;
+}
+
 // ------------------------------------------------------------------------- combiners
 
 enum class Post : int { Write = 0, Mean = 1, Accum = 2 };
@@ -208,11 +247,13 @@ __device__ __forceinline__ void store_final(void *out, int64_t off, const typena
 
 // The i-th term of a serial refold. A storing producer's terms are read back from where it stored
 // them (only a sum over a leading axis refolds one, after its workgroup or launch has stored every
-// term of the column): its inputs may have been overwritten by those stores (dc written over dout).
+// term of the column): its inputs may have been overwritten by those stores (dc written over
+// dout). One with kRefoldInputs stores something other than its terms, over none of the operands
+// its terms read, and recomputes them.
 template <class Prod, int NIN>
 __device__ __forceinline__ float value_at(const RedArgs<NIN> &A, const Prod &prod,
                                           const int64_t *base, uint64_t i) {
-  if constexpr (kStores<Prod>) {
+  if constexpr (kStores<Prod> && !StoresOther<Prod>::value) {
     return prod.dst[base[0] + int64_t(i) * A.rst[0]];
   } else {
     float v[NIN];
@@ -582,7 +623,7 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
 #pragma unroll
         for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
         const float y = prod.eval(v);
-        yv[c] = y;
+        yv[c] = stored_value(prod, v, y);
         if constexpr (kExt) {
           f[c].m = IS_MAX ? fmaxf(f[c].m, y) : fminf(f[c].m, y);
           f[c].nan |= y != y ? 1u : 0u;
@@ -696,8 +737,9 @@ __global__ __launch_bounds__(kBlock) void red_cols_small_kernel(RedArgs<Prod::NI
         float v[NIN];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) v[k] = xv[u][k][c];
-        yv[c] = prod.eval(v);
-        f[c] = f[c] + yv[c];
+        const float y = prod.eval(v);
+        f[c] = f[c] + y;
+        yv[c] = stored_value(prod, v, y);
       }
       if constexpr (kStores<Prod>)  // a storing producer also writes each value it sums
         *reinterpret_cast<f4 *>(prod.dst + base[0] + int64_t(r) * A.rst[0]) = yv;

@@ -3,8 +3,9 @@
 // tests/test_fusion_pass.py against no-op kernel stubs (the pass only rewrites structs).
 //
 // Each trial builds a random DAG in topological order: unary and binary elementwise nodes over
-// GPU fp32 tensors of broadcast-compatible shapes, with random fan-out, and nodes the pass must
-// leave alone (an output that requires grad, an input on the CPU, a non-elementwise op). It
+// GPU fp32 tensors of broadcast-compatible shapes, with random fan-out, leaky slopes of either
+// sign, gradients required by some leaves (and by every tensor computed from one), and nodes the
+// pass must leave alone (an input on the CPU, a non-elementwise op). It
 // evaluates the DAG node by node on the host, runs the pass, evaluates the rewritten DAG (fused
 // nodes through a restatement of the tape's semantics, include/plast_hip.h: PlastTapeOp) and
 // requires:
@@ -13,8 +14,11 @@
 //   - the rewritten DAG to be in topological order, each fused node to have 2..MAX_INS
 //     instructions and at most MAX_INPUTS inputs, and the node count to drop by the fused chains'
 //     lengths minus one;
-//   - no fused node to hold an op the pass must not touch.
-// Prints "ok <trials> <fused chains>" or the first failure, and exits non-zero on failure.
+//   - no fused node to hold an op the pass must not touch, and a fused node with a gradient to be
+//     exactly leaky_relu(x + bias, slope >= 0): x of the output's shape, the bias a row of its
+//     last extent (the only chain whose backward the library has).
+// Prints "ok <trials> <fused chains> <of them with gradients>" or the first failures, and exits
+// non-zero on failure.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -117,6 +121,31 @@ OP_TYPE binary_of_tape(u8 op) {
 
 bool is_tape_binary(u8 op) { return op == TAPE_ADD || op == TAPE_SUB || op == TAPE_MUL || op == TAPE_DIV; }
 
+bool same_extents(const Tensor *a, const Tensor *b) {
+  if (a->ndim != b->ndim) return false;
+  for (u64 d = 0; d < a->ndim; ++d)
+    if (a->shape[d] != b->shape[d]) return false;
+  return true;
+}
+
+// The one fused chain allowed to carry a gradient: LOAD, ADD of the other input, LEAKY_RELU with
+// a slope >= 0, over x (the output's extents) and a bias row (the output's last extent, 1 before).
+bool leaky_bias_node(const Node *n) {
+  const PlastFusedTape *tp = reinterpret_cast<const PlastFusedTape *>(uintptr_t(n->params.dim));
+  if (n->num_inputs != 2 || tp->num_ins != 3 || tp->ins[0].op != TAPE_LOAD ||
+      tp->ins[1].op != TAPE_ADD || tp->ins[1].src != TAPE_SRC_INPUT ||
+      tp->ins[2].op != TAPE_LEAKY_RELU || !(tp->ins[2].imm >= 0.0f))
+    return false;
+  const Tensor *y = n->output;
+  for (int k = 0; k < 2; ++k) {
+    const Tensor *x = n->inputs[k], *b = n->inputs[1 - k];
+    bool row = b->ndim >= 1 && b->ndim <= y->ndim && b->shape[b->ndim - 1] == y->shape[y->ndim - 1];
+    for (u64 d = 0; row && d + 1 < b->ndim; ++d) row = b->shape[d] == 1;
+    if (same_extents(x, y) && row) return true;
+  }
+  return false;
+}
+
 // A node of the harness: its struct, and an opaque op the pass may not fuse (evaluated as a copy
 // of its input) when `opaque`.
 struct N {
@@ -177,7 +206,7 @@ int main(int argc, char **argv) {
   auto pick = [&](int n) { return int(rng() % unsigned(n)); };
   const OP_TYPE un[] = {LEAKY_RELU, EXP, LOG, NEG, ABS, SIN, COS, TAN};
   const OP_TYPE bin[] = {ADD, SUB, MUL, DIV};
-  long total_fused = 0;
+  long total_fused = 0, grad_pairs = 0;
   for (int trial = 0; trial < trials; ++trial) {
     std::vector<std::unique_ptr<T>> ts;
     std::vector<std::unique_ptr<N>> ns;
@@ -194,8 +223,46 @@ int main(int argc, char **argv) {
       else make(*x, 1, C, 1);
       for (float &f : x->v) f = float(int(rng() % 2001) - 1000) / 250.0f + (pick(7) == 0 ? 0.0f : 0.5f);
       if (pick(12) == 0) x->t.device = CPU;
+      if (pick(5) == 0) x->t.requires_grad = true;
       avail.push_back(&x->t);
       ts.push_back(std::move(x));
+    }
+    // in some trials an explicit leaky_relu(x + bias) pair first (either operand order, a slope of
+    // either sign), which random DAGs rarely hold
+    if (pick(3) == 0) {
+      Tensor *x = nullptr, *b = nullptr;
+      for (Tensor *t : avail) {
+        const T *o = owner_of(ts, t);
+        if (!x && o->rows == R && o->cols == C && t->ndim == 2) x = t;
+        else if (!b && o->rows == 1 && o->cols == C) b = t;
+      }
+      if (x && b) {
+        Tensor *prev = nullptr;
+        for (int k = 0; k < 2; ++k) {
+          auto nd = std::make_unique<N>();
+          memset(&nd->n, 0, sizeof nd->n);
+          auto o = std::make_unique<T>();
+          make(*o, R, C, 2);
+          if (k == 0) {
+            nd->n.op_type = ADD;
+            nd->ins = pick(2) ? std::vector<Tensor *>{x, b} : std::vector<Tensor *>{b, x};
+          } else {
+            nd->n.op_type = LEAKY_RELU;
+            nd->n.params.fval = 0.01f * float(pick(50) - 10);
+            nd->ins = {prev};
+          }
+          for (Tensor *in : nd->ins) o->t.requires_grad = o->t.requires_grad || in->requires_grad;
+          nd->n.inputs = nd->ins.data();
+          nd->n.num_inputs = int(nd->ins.size());
+          nd->n.output = &o->t;
+          nd->n.op = plast_hip_get_op_impl(nd->n.op_type);
+          o->t.creator = &nd->n;
+          prev = &o->t;
+          avail.push_back(&o->t);
+          ts.push_back(std::move(o));
+          ns.push_back(std::move(nd));
+        }
+      }
     }
     const int nnodes = 2 + pick(14);
     for (int q = 0; q < nnodes; ++q) {
@@ -226,14 +293,14 @@ int main(int argc, char **argv) {
       } else {
         make(*o, ta->rows, ta->cols, 2);
         nd->n.op_type = un[pick(8)];
-        nd->n.params.fval = 0.01f * float(pick(50));
+        nd->n.params.fval = 0.01f * float(pick(50) - 10);
         nd->ins = {a};
         if (kind == 9) {  // an op the pass must not fuse (a reduction slot, evaluated as a copy)
           nd->n.op_type = SUM;
           nd->opaque = true;
         }
       }
-      if (pick(15) == 0) o->t.requires_grad = true;
+      for (Tensor *in : nd->ins) o->t.requires_grad = o->t.requires_grad || in->requires_grad;
       nd->n.inputs = nd->ins.data();
       nd->n.num_inputs = int(nd->ins.size());
       nd->n.output = &o->t;
@@ -290,9 +357,15 @@ int main(int argc, char **argv) {
         }
         dropped += members - 1;
         CHECK(n->output->creator == n, "fused output's creator is not the fused node");
-        for (int k = 0; k < n->num_inputs; ++k)
-          CHECK(n->inputs[k]->device == GPU && !n->inputs[k]->requires_grad, "fused a CPU or grad input");
-        CHECK(!n->output->requires_grad, "fused an output that requires grad");
+        bool grads = n->output->requires_grad;
+        for (int k = 0; k < n->num_inputs; ++k) {
+          CHECK(n->inputs[k]->device == GPU, "fused a CPU input");
+          grads = grads || n->inputs[k]->requires_grad;
+        }
+        if (grads) {
+          CHECK(leaky_bias_node(n), "fused a chain with gradients that is not leaky_relu(x + bias)");
+          ++grad_pairs;
+        }
       } else {
         for (auto &nd : ns)
           if (&nd->n == n && nd->opaque) CHECK(n->op_type == SUM, "opaque node changed");
@@ -321,6 +394,6 @@ int main(int argc, char **argv) {
     std::printf("FAILED %d checks\n", fails);
     return 1;
   }
-  std::printf("ok %d %ld\n", trials, total_fused);
+  std::printf("ok %d %ld %ld\n", trials, total_fused, grad_pairs);
   return 0;
 }

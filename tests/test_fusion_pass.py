@@ -39,7 +39,8 @@ def _build(tmp_path, ops_src: str, tag: str) -> Path:
 def _ops_src() -> str:
     # the pass as committed; its include is made absolute so a copy elsewhere builds the same
     return (ROOT / "plast_amd" / "csrc" / "ops.cpp").read_text().replace(
-        '"../../include/plast_hip.h"', '"plast_hip.h"')
+        '"../../include/plast_hip.h"', '"plast_hip.h"').replace(
+        '"fused_grad.hpp"', f'"{ROOT / "plast_amd" / "csrc" / "fused_grad.hpp"}"')
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
@@ -47,8 +48,9 @@ def test_fusion_pass_fuzz(tmp_path):
     exe = _build(tmp_path, _ops_src(), "committed")
     r = subprocess.run([str(exe), "3000"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
-    trials, fused = map(int, r.stdout.split()[1:3])
+    trials, fused, grad_pairs = map(int, r.stdout.split()[1:4])
     assert fused > trials // 4, f"only {fused} chains fused over {trials} DAGs: the DAGs rarely chain"
+    assert grad_pairs > 20, f"only {grad_pairs} leaky_relu(x + bias) pairs with gradients fused"
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
@@ -61,3 +63,16 @@ def test_fusion_fuzz_catches_a_swapped_operand(tmp_path):
     exe = _build(tmp_path, planted, "planted")
     r = subprocess.run([str(exe), "3000"], capture_output=True, text=True, timeout=300)
     assert r.returncode != 0 and "differs after fusion" in r.stdout, r.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_fusion_fuzz_catches_a_negative_slope_pair(tmp_path):
+    """A copy of the pass that fuses leaky_relu(x + bias) with gradients for any slope (whose
+    backward could not read its mask from the output when the slope is negative) must fail the
+    harness."""
+    src = _ops_src()
+    planted = src.replace("!plast::fused_grad::alpha_ok(nodes[l]->params.fval) ||", "")
+    assert planted != src
+    exe = _build(tmp_path, planted, "slope")
+    r = subprocess.run([str(exe), "3000"], capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0 and "not leaky_relu(x + bias)" in r.stdout, r.stdout

@@ -9,16 +9,20 @@ tensors on device 1: the HIP kernels.
 Checked against the oracle:
   config 2's five-node chain, fused by the pass into one FUSED_ELEMENTWISE node (exp within 2 ulp,
   the rest bit for bit);
-  config 1's training step relu(X + b) (not fused: it requires grad), its backward with an upstream
-  gradient, dX bit for bit and the bias gradient within 1e-5 of sum_rows |terms| (the reference's
-  broadcast accumulation order is unspecified);
-  config 2's chain as a training graph (five unfused nodes forward and backward), every leaf
-  gradient within 4 ulp (each passes through exp's backward, which multiplies by exp's output,
-  itself within 2 ulp).
+  config 1's training step leaky_relu(X + b) with gradients, fused by the pass into one node whose
+  backward writes dX and adds the bias's column sum in one pass: Y and dX bit for bit, the bias
+  gradient within 1e-5 of sum_rows |terms| (the reference's broadcast accumulation order is
+  unspecified), over both operand orders, either gradient alone, slopes 0 and > 0, a rank-3 X,
+  odd column counts, one row, and values where IEEE rules decide the mask and the sums;
+  config 2's chain as a training graph (its ADD -> LEAKY_RELU pair fused with gradients, the other
+  three nodes unfused, forward and backward), every leaf gradient within 4 ulp (each passes
+  through exp's backward, which multiplies by exp's output, itself within 2 ulp).
 
 Needs oracle/_ref/libplast_ref.so, built in a container that holds the reference's sources; skipped
 where it is absent."""
 from __future__ import annotations
+
+import zlib
 
 import numpy as np
 import pytest
@@ -75,40 +79,95 @@ def test_config2_chain_fused_by_the_pass_runs_in_the_reference_dag_forward():
     assert _ulp(got, hts["t4"].numpy()).max() <= 2
 
 
-def test_config1_training_step_through_the_reference_executor():
+def _plant_specials(x, bias, gy):
+    """Values where the mask or the sums are decided by IEEE rules: x + b overflowing to +-inf
+    (with slope 0, -inf * 0 is NaN in y), NaN inputs, exact zeros of both signs, infinite and NaN
+    upstream gradients."""
+    x2, g2 = x.reshape(-1, x.shape[-1]), gy.reshape(-1, gy.shape[-1])
+    C = x2.shape[1]
+    if C < 8 or x2.shape[0] < 3:
+        return
+    bias[0], bias[1] = 3.0e38, -3.0e38
+    x2[0, 0], x2[1, 1] = 3.0e38, -3.0e38
+    x2[2, 2] = np.nan
+    x2[0, 3], bias[3] = np.float32(-0.5), np.float32(0.5)     # x + b == +0
+    x2[1, 4], bias[4] = np.float32(-0.0), np.float32(-0.0)    # x + b == -0
+    g2[2, 5], g2[1, 6], g2[0, 7] = np.inf, np.nan, -0.0
+
+
+CONFIG1_CASES = [
+    # (name, x shape, slope, x grad, bias grad, bias first, bias 1-D, prefilled grads, specials)
+    ("config1", (1024, 256), 0.0, True, True, False, True, False, False),
+    ("leaky_bias_first", (1000, 260), 0.01, True, True, True, True, True, True),
+    ("x_grad_only", (333, 132), 0.2, True, False, False, True, True, True),
+    ("bias_grad_only", (333, 132), 0.0, False, True, True, False, True, True),
+    ("rank3_odd_columns", (4, 37, 130), 0.0, True, True, False, True, True, True),
+    ("one_row", (1, 4096), 0.1, True, True, False, False, True, False),
+    ("many_rows", (16384, 64), 0.0, True, True, False, True, True, True),
+]
+
+
+@pytest.mark.parametrize("name, shape, alpha, gx, gb, bias_first, bias_1d, prefill, specials",
+                         CONFIG1_CASES, ids=[c[0] for c in CONFIG1_CASES])
+def test_config1_training_step_fused_through_the_reference_executor(
+        name, shape, alpha, gx, gb, bias_first, bias_1d, prefill, specials):
+    """leaky_relu(X + b) with gradients: the pass fuses the pair into one FUSED_ELEMENTWISE node
+    (forward one launch writing Y only; backward one pass writing dX and adding the bias's column
+    sum), run by the reference's dag_forward / dag_backward and checked against the unfused
+    oracle: Y and dX bit for bit, the bias gradient within 1e-5 of sum_rows |terms| (the
+    reference's broadcast accumulation order is unspecified). Gradients already holding values
+    are added to, as the reference's backwards add."""
     from plast_amd import runtime as rt
-    print("reference executor: config 1 training step", flush=True)
-    rng = np.random.RandomState(12)
-    x = rng.uniform(-1, 1, (1024, 256)).astype(np.float32)
-    bias = rng.uniform(-1, 1, 256).astype(np.float32)
-    gy = rng.uniform(-1, 1, (1024, 256)).astype(np.float32)
-    X, B = rt.DeviceTensor.from_numpy(x, True), rt.DeviceTensor.from_numpy(bias, True)
-    S = rt.DeviceTensor((1024, 256), requires_grad=True, zero=False)
-    Y = rt.DeviceTensor((1024, 256), requires_grad=True, zero=False)
+    print(f"reference executor: fused leaky_relu(X + b) {name} {shape}", flush=True)
+    rng = np.random.RandomState(zlib.crc32(name.encode()) % 1000)
+    C = shape[-1]
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    bias = rng.uniform(-1, 1, C if bias_1d else (1, C)).astype(np.float32)
+    gy = rng.uniform(-1, 1, shape).astype(np.float32)
+    if specials:
+        _plant_specials(x, bias.reshape(-1), gy)
+    gx0 = rng.uniform(-1, 1, shape).astype(np.float32) if prefill else np.zeros(shape, np.float32)
+    gb0 = (rng.uniform(-1, 1, bias.shape).astype(np.float32) if prefill
+           else np.zeros(bias.shape, np.float32))
+    X, B = rt.DeviceTensor.from_numpy(x, gx), rt.DeviceTensor.from_numpy(bias, gb)
+    if gx:
+        rt.lib().arena_memcpy_h2d_hip(X.grad.ptr, gx0.ctypes.data, gx0.nbytes)
+    if gb:
+        rt.lib().arena_memcpy_h2d_hip(B.grad.ptr, gb0.ctypes.data, gb0.nbytes)
+    S = rt.DeviceTensor(shape, requires_grad=True, zero=False)
+    Y = rt.DeviceTensor(shape, requires_grad=True, zero=False)
     g = RefGraph()
     try:
-        g.node("add", [X, B], S)
-        g.node("leaky_relu", [S], Y, KernelParams(0, 0, 0.0))
-        assert g.build(fuse=True) == 0          # requires grad: left for the backward
-        assert g.op_types() == ["ADD", "LEAKY_RELU"]
+        g.node("add", [B, X] if bias_first else [X, B], S)
+        g.node("leaky_relu", [S], Y, KernelParams(0, 0, alpha))
+        assert g.build(fuse=True) == 1
+        assert g.op_types() == ["FUSED_ELEMENTWISE"], g.op_types()
         g.forward()
         rt.lib().arena_memcpy_h2d_hip(Y.grad.ptr, gy.ctypes.data, gy.nbytes)
         g.backward()
-        y, dx, db = Y.numpy(), X.grad.numpy(), B.grad.numpy()
+        y = Y.numpy()
+        dx = X.grad.numpy() if gx else None
+        db = B.grad.numpy() if gb else None
     finally:
         g.close()
     hx, hb = HostTensor(x, requires_grad=True), HostTensor(bias, requires_grad=True)
+    hx.grad.buf[:] = gx0.reshape(-1)
+    hb.grad.buf[:] = gb0.reshape(-1)
     hs = HostTensor(np.zeros_like(x), requires_grad=True)
     hy = HostTensor(np.zeros_like(x), requires_grad=True)
-    oracle_forward("add", [hx, hb], hs)
-    oracle_forward("leaky_relu", [hs], hy, KernelParams(0, 0, 0.0))
+    ins = [hb, hx] if bias_first else [hx, hb]
+    oracle_forward("add", ins, hs)
+    oracle_forward("leaky_relu", [hs], hy, KernelParams(0, 0, alpha))
     hy.grad.buf[:] = gy.reshape(-1)
-    oracle_backward("leaky_relu", [hs], hy, KernelParams(0, 0, 0.0))
-    oracle_backward("add", [hx, hb], hs)
-    assert_bits(y, hy.numpy(), "relu(X + b)")
-    assert_bits(dx, hx.grad.numpy(), "dX")
-    scale = np.abs(hs.grad.numpy()).sum(axis=0)
-    assert_close_sum(db, hb.grad.numpy(), scale, 1e-5, "db")
+    oracle_backward("leaky_relu", [hs], hy, KernelParams(0, 0, alpha))
+    oracle_backward("add", ins, hs)
+    assert_bits(y, hy.numpy(), "leaky_relu(X + b)")
+    if gx:
+        assert_bits(dx, hx.grad.numpy(), "dX")
+    if gb:
+        scale = np.abs(hs.grad.numpy().astype(np.float64)).reshape(-1, C).sum(axis=0)
+        scale = scale + np.abs(gb0.astype(np.float64)).reshape(-1)
+        assert_close_sum(db.reshape(-1), hb.grad.numpy().reshape(-1), scale, 1e-5, "db")
 
 
 def test_config2_chain_as_a_training_graph():
@@ -122,8 +181,10 @@ def test_config2_chain_as_a_training_graph():
     g = RefGraph()
     try:
         ts = _chain(g, leaves, n, True, rt)
-        assert g.build(fuse=True) == 0
-        assert g.op_types() == ["MUL", "ADD", "LEAKY_RELU", "NEG", "EXP"]
+        # ADD(a*b, c) -> LEAKY_RELU is the pair the pass fuses with gradients (c, of the output's
+        # extent, is a one-row bias); the other nodes stay, as they require grad
+        assert g.build(fuse=True) == 1
+        assert g.op_types() == ["MUL", "FUSED_ELEMENTWISE", "NEG", "EXP"], g.op_types()
         g.forward()
         rt.lib().arena_memcpy_h2d_hip(ts["t4"].grad.ptr, gy.ctypes.data, gy.nbytes)
         g.backward()
