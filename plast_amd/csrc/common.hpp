@@ -72,17 +72,29 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // 1536 and fewer leave CUs idle.
 #define PLAST_ROW_WAVES 2048
 #endif
-// Rows in flight per lane, leading-axis reductions, for one-operand and two-operand producers.
+// Rows in flight per lane, leading-axis reductions, for one-, two- and three-operand producers.
 // Measured (two alternating runs): one operand with 2 rather than 4 rows, the axis-0 sum of
 // [4096, 65536] 6.60-6.64 -> 6.72-6.74 TB/s, config 5's bias gradient 6.24-6.26 -> 6.41-6.42, the
 // [16384, 4096] bias gradient 5.24-5.31 -> 5.61-5.64 (1 row loses 11-17% on the first two); two
 // operands (the one-pass relu-gradient modulation and bias sum) 5.38-5.65 with 4 rows, 5.59-5.82
-// with 2, 6.02-6.06 with 1.
+// with 2, 6.02-6.06 with 1. Three operands (the fused leaky_relu(x + bias) backward, the
+// [16384, 4096] step, in one process): 2 rows 6.00-6.01 TB/s against 5.77-5.91 with 1.
 #ifndef PLAST_COL_UNROLL
 #define PLAST_COL_UNROLL 2
 #endif
 #ifndef PLAST_COL_UNROLL2
 #define PLAST_COL_UNROLL2 1
+#endif
+#ifndef PLAST_COL_UNROLL3
+#define PLAST_COL_UNROLL3 2  // three operands and more
+#endif
+// Stores of a storing producer in the leading-axis kernels (1: nontemporal, 0: ordinary, -1:
+// nontemporal exactly when the stored buffer is also an operand, read in the same pass). Measured
+// in one process on [16384, 4096]: the fused leaky_relu(x + bias) step (dx read and written)
+// 5.36-5.41 -> 5.91-5.92 TB/s with nontemporal stores; the one-pass epilogue (dc only written)
+// 6.25-6.28 -> 5.94 with them.
+#ifndef PLAST_COL_NT_STORE
+#define PLAST_COL_NT_STORE -1
 #endif
 // Leading-axis finalize: lanes per output when there are at least twice as many chunks (1: one
 // lane, batches of 16 loads in sequence). Measured (two alternating runs): 8 lanes took config 1's
@@ -94,12 +106,34 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #define PLAST_COL_FIN_Q 16
 #endif
 // Small leading-axis sums (at most PLAST_COL_SMALL_MAX input elements) in one launch: workgroups
-// of PLAST_COL_SMALL_S4 float4 columns that walk every row, instead of row chunks plus a finalize.
+// of PLAST_COL_SMALL_S4 float4 columns (PLAST_COL_SMALL_S4_3 for three operands and more) that
+// walk every row, instead of row chunks plus a finalize; PLAST_COL_SMALL3 = 0 sends three-operand
+// producers to the chunked pass, whose chunks keep at least PLAST_COL_MIN_ROWS3 rows.
+// PLAST_COL_SMALL_XCD numbers the column slices per XCD, so that the slices sharing a 128-byte
+// line run on one XCD. Measured in one process (device time of calls replayed from a graph),
+// config 1's fused step [1024, 256] (the forward, then the backward's 3-operand sum) in GB/s:
+// slices of 4 float4 columns 403, of 1 float4 column 453 without and 589 with the numbering,
+// against 571 for the chunked pass (16-row chunks) with its finalize launch and 475 for that pass
+// with the last workgroup merging the partials itself (a device-scope fence per workgroup; it
+// also cost the [16384, 4096] sums 25-40%, and was removed). Config 1's grad_b (1 operand):
+// 355 -> 386 with 2 float4 columns per slice and the numbering.
 #ifndef PLAST_COL_SMALL_MAX
 #define PLAST_COL_SMALL_MAX (1u << 21)
 #endif
 #ifndef PLAST_COL_SMALL_S4
-#define PLAST_COL_SMALL_S4 4
+#define PLAST_COL_SMALL_S4 2
+#endif
+#ifndef PLAST_COL_SMALL_S4_3
+#define PLAST_COL_SMALL_S4_3 1
+#endif
+#ifndef PLAST_COL_SMALL3
+#define PLAST_COL_SMALL3 1
+#endif
+#ifndef PLAST_COL_MIN_ROWS3
+#define PLAST_COL_MIN_ROWS3 64
+#endif
+#ifndef PLAST_COL_SMALL_XCD
+#define PLAST_COL_SMALL_XCD 1
 #endif
 // Workgroups a leading-axis reduction is chunked up to (512, 2048 and 4096 measured slower on every
 // leading-axis workload of the bench). A row stream for whole contiguous rows

@@ -476,16 +476,22 @@ __device__ __forceinline__ typename Comb::Part merge_in_order(const typename Com
                                                               uint64_t stride, uint32_t segs) {
   using Part = typename Comb::Part;
   constexpr uint32_t kBatch = 16;
-  Part p = part[0];
-  uint32_t s = 1;
-  for (; s + kBatch <= segs; s += kBatch) {
+  // whole batches of loads, the last one clamped to the final partial (loaded, not merged): a
+  // partial batch of one-at-a-time loads would wait out a memory latency per partial
+  Part p{};
+  for (uint32_t s = 0; s < segs; s += kBatch) {
     Part q[kBatch];
 #pragma unroll
-    for (uint32_t i = 0; i < kBatch; ++i) q[i] = part[uint64_t(s + i) * stride];
+    for (uint32_t i = 0; i < kBatch; ++i) {
+      const uint32_t k = s + i < segs ? s + i : segs - 1;
+      q[i] = part[uint64_t(k) * stride];
+    }
 #pragma unroll
-    for (uint32_t i = 0; i < kBatch; ++i) p = Comb::merge(p, q[i]);
+    for (uint32_t i = 0; i < kBatch; ++i) {
+      if (s + i == 0) p = q[0];
+      else if (s + i < segs) p = Comb::merge(p, q[i]);
+    }
   }
-  for (; s < segs; ++s) p = Comb::merge(p, part[uint64_t(s) * stride]);
   return p;
 }
 
@@ -539,7 +545,21 @@ __global__ __launch_bounds__(kBlock) void red_rows_finalize(RedArgs<Prod::NIN> A
 // ------------------------------------------------------------------------- cols kernel
 
 template <class Prod>
-constexpr int kColUnroll = Prod::NIN == 1 ? PLAST_COL_UNROLL : PLAST_COL_UNROLL2;
+constexpr int kColUnroll = Prod::NIN == 1   ? PLAST_COL_UNROLL
+                           : Prod::NIN == 2 ? PLAST_COL_UNROLL2
+                                            : PLAST_COL_UNROLL3;
+
+template <class Prod>
+__device__ __forceinline__ void store_col(f4 *p, f4 v) {
+  constexpr bool nt = PLAST_COL_NT_STORE == 1 || (PLAST_COL_NT_STORE == -1 && StoresOther<Prod>::value);
+  if constexpr (nt) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+template <class Prod>
+constexpr int kColMinRows = Prod::NIN >= 3 ? PLAST_COL_MIN_ROWS3 : 64;
+template <class Prod>
+constexpr int kColSmallS4 = Prod::NIN >= 3 ? PLAST_COL_SMALL_S4_3 : PLAST_COL_SMALL_S4;
 
 // Fast summary of an order-sensitive fold (exact max/min): the plain extreme and a NaN flag.
 struct ExtFast {
@@ -555,7 +575,9 @@ struct ExtFast {
 // merge directly. The exact max/min fold keeps a plain extreme and a NaN flag per wave, and a
 // column is refolded serially in index order only when its chunk holds a NaN or its extreme is
 // zero (the cases where order decides the bits).
-template <class Prod, class Comb, bool VEC>
+// ALLV (with VEC): every operand is streamed with float4 loads, so the loads take no branch on
+// the operand mask (a broadcast operand's splat makes the compiler wait for each load in turn).
+template <class Prod, class Comb, bool VEC, bool ALLV>
 __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, Prod prod,
                                                           uint32_t xblocks) {
   constexpr int NIN = Prod::NIN;
@@ -578,10 +600,15 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   const uint32_t o = bx / xblocks;
   const uint64_t j = (uint64_t(bx - o * xblocks) * 64 + lane) * W;
   const bool active = j < A.inner;  // no early return: the workgroup meets at a barrier
-  int64_t base[NIN], tbase;
+  int64_t base[NIN], lbase[NIN], tbase;
   decode_outer(A, o, base, tbase);
 #pragma unroll
-  for (int k = 0; k < NIN; ++k) base[k] += int64_t(j) * A.kst[k];
+  for (int k = 0; k < NIN; ++k) {
+    // an inactive lane loads column 0 (in bounds) and drops it: the loads take no branch
+    lbase[k] = base[k];
+    base[k] += int64_t(j) * A.kst[k];
+    if (active) lbase[k] = base[k];
+  }
   const uint64_t k0 = uint64_t(chunk) * A.seglen;
   const uint64_t k1 = k0 + A.seglen < A.len ? k0 + A.seglen : A.len;
 
@@ -596,13 +623,13 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
     float xv[kU][NIN][W];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const uint64_t r = r0 + 4 * u;
-      if (!active || r >= k1) continue;
+      // a row past the chunk is clamped to its last row: loaded, not used
+      const uint64_t r = r0 + 4 * u < k1 ? r0 + 4 * u : k1 - 1;
 #pragma unroll
       for (int k = 0; k < NIN; ++k) {
-        const float *src = A.in[k] + base[k] + int64_t(r) * A.rst[k];
+        const float *src = A.in[k] + lbase[k] + int64_t(r) * A.rst[k];
         if constexpr (VEC) {
-          const f4 v = (A.vec_mask >> k & 1u)
+          const f4 v = (ALLV || (A.vec_mask >> k & 1u))
                            ? __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src))
                            : f4(src[0]);
 #pragma unroll
@@ -633,8 +660,10 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
       }
       if constexpr (kStores<Prod>) {
         float *dst = prod.dst + base[0] + int64_t(r) * A.rst[0];
-        if constexpr (VEC) *reinterpret_cast<f4 *>(dst) = f4{yv[0], yv[1], yv[2], yv[3]};
-        else dst[0] = yv[0];
+        if constexpr (VEC)
+          store_col<Prod>(reinterpret_cast<f4 *>(dst), f4{yv[0], yv[1], yv[2], yv[3]});
+        else
+          dst[0] = yv[0];
       }
     }
   }
@@ -698,33 +727,40 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
 // of float4 column c in order. The row groups of a wave then merge with a fixed butterfly, and the
 // four waves' partials in wave order: the result is deterministic. A column whose sum is not finite
 // is summed again serially in index order (the reference's order decides such sums).
-template <class Prod>
+template <class Prod, bool ALLV>
 __global__ __launch_bounds__(kBlock) void red_cols_small_kernel(RedArgs<Prod::NIN> A, Prod prod,
                                                                 uint32_t xblocks) {
   constexpr int NIN = Prod::NIN;
-  constexpr int S4 = PLAST_COL_SMALL_S4, G = kBlock / S4, kU = 8;
+  constexpr int S4 = kColSmallS4<Prod>, G = kBlock / S4, kU = 8;
   static_assert(64 % S4 == 0, "row groups split evenly over the waves");
   __shared__ f4 sh[kBlock / 64][S4];
   const uint32_t t = threadIdx.x, c4 = t % S4, g = t / S4, lane = t & 63, wv = t >> 6;
-  const uint32_t o = blockIdx.x / xblocks;
-  const uint64_t j0 = uint64_t(blockIdx.x - o * xblocks) * (4 * S4);  // the slice's first column
+  // XCD numbering: the workgroups of one XCD take adjacent column slices, so the slices that share
+  // a cache line share that XCD's L2
+  const uint32_t b = PLAST_COL_SMALL_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint32_t o = b / xblocks;
+  const uint64_t j0 = uint64_t(b - o * xblocks) * (4 * S4);  // the slice's first column
   const uint64_t j = j0 + 4 * c4;
   const bool active = j < A.inner;
-  int64_t base0[NIN], base[NIN], tbase;
+  int64_t base0[NIN], base[NIN], lbase[NIN], tbase;
   decode_outer(A, o, base0, tbase);
 #pragma unroll
-  for (int k = 0; k < NIN; ++k) base[k] = base0[k] + int64_t(j) * A.kst[k];
+  for (int k = 0; k < NIN; ++k) {
+    base[k] = base0[k] + int64_t(j) * A.kst[k];
+    lbase[k] = active ? base[k] : base0[k];  // an inactive lane loads column 0 and drops it
+  }
   f4 f = f4(0.0f);
   for (uint64_t r0 = g; r0 < A.len; r0 += uint64_t(G) * kU) {
     f4 xv[kU][NIN];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const uint64_t r = r0 + uint64_t(u) * G;
-      if (!active || r >= A.len) continue;
+      // rows past the end are clamped to the last row: loaded, not used (the loads take no branch)
+      const uint64_t r = r0 + uint64_t(u) * G < A.len ? r0 + uint64_t(u) * G : A.len - 1;
 #pragma unroll
       for (int k = 0; k < NIN; ++k) {
-        const float *src = A.in[k] + base[k] + int64_t(r) * A.rst[k];
-        xv[u][k] = (A.vec_mask >> k & 1u) ? *reinterpret_cast<const f4 *>(src) : f4(src[0]);
+        const float *src = A.in[k] + lbase[k] + int64_t(r) * A.rst[k];
+        xv[u][k] = (ALLV || (A.vec_mask >> k & 1u)) ? *reinterpret_cast<const f4 *>(src)
+                                                    : f4(src[0]);
       }
     }
 #pragma unroll
@@ -742,7 +778,7 @@ __global__ __launch_bounds__(kBlock) void red_cols_small_kernel(RedArgs<Prod::NI
         yv[c] = stored_value(prod, v, y);
       }
       if constexpr (kStores<Prod>)  // a storing producer also writes each value it sums
-        *reinterpret_cast<f4 *>(prod.dst + base[0] + int64_t(r) * A.rst[0]) = yv;
+        store_col<Prod>(reinterpret_cast<f4 *>(prod.dst + base[0] + int64_t(r) * A.rst[0]), yv);
     }
   }
   // the wave's row groups (lanes c4, c4 + S4, ...) merge pairwise with a fixed butterfly
@@ -1038,15 +1074,17 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
       }
     }
     A.rows = nout / A.inner;  // outer count
+    const bool allv = A.vec_mask == (1u << NIN) - 1;
     const uint32_t W = vec ? 4 : 1;
     const uint32_t xblocks = ceil_div(A.inner, uint64_t(64) * W);
     const uint64_t base_blocks = uint64_t(xblocks) * A.rows;
-    // chunk the reduced axis until the grid has ~PLAST_COL_BLOCKS workgroups, keeping >= 64 rows
-    // per chunk
+    // chunk the reduced axis until the grid has ~PLAST_COL_BLOCKS workgroups, keeping at least
+    // kColMinRows rows per chunk
     uint64_t chunks = 1;
-    if (base_blocks < PLAST_COL_BLOCKS && A.len >= 128) {
+    constexpr uint64_t min_rows = kColMinRows<Prod>;
+    if (base_blocks < PLAST_COL_BLOCKS && A.len >= 2 * min_rows) {
       chunks = (PLAST_COL_BLOCKS + base_blocks - 1) / base_blocks;
-      const uint64_t max_c = A.len / 64;
+      const uint64_t max_c = A.len / min_rows;
       if (chunks > max_c) chunks = max_c;
       if (chunks > 65535) chunks = 65535;
       if (chunks < 1) chunks = 1;
@@ -1059,10 +1097,12 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
     A.divisor = divisor;
     if constexpr (std::is_same<Comb, SumComb>::value) {
       // small: one launch over narrow column slices instead of chunks plus a finalize
-      if (chunks > 1 && vec && A.len * nout <= PLAST_COL_SMALL_MAX) {
-        const uint32_t sblocks = ceil_div(A.inner, uint64_t(4) * PLAST_COL_SMALL_S4);
-        red_cols_small_kernel<Prod><<<unsigned(uint64_t(sblocks) * A.rows), kBlock, 0, stream()>>>(
-            A, prod, sblocks);
+      if (chunks > 1 && vec && A.len * nout <= PLAST_COL_SMALL_MAX &&
+          (NIN < 3 || PLAST_COL_SMALL3 != 0)) {
+        const uint32_t sblocks = ceil_div(A.inner, uint64_t(4) * kColSmallS4<Prod>);
+        const unsigned grid = unsigned(uint64_t(sblocks) * A.rows);
+        if (allv) red_cols_small_kernel<Prod, true><<<grid, kBlock, 0, stream()>>>(A, prod, sblocks);
+        else red_cols_small_kernel<Prod, false><<<grid, kBlock, 0, stream()>>>(A, prod, sblocks);
         return true;
       }
     }
@@ -1072,8 +1112,12 @@ bool launch_reduction(const Prod &prod, const void *const *in, void *out, Space 
         if (!A.part) return false;
       }
       const dim3 grid{unsigned(base_blocks), unsigned(chunks), 1u};
-      if (vec) red_cols_kernel<Prod, Comb, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
-      else red_cols_kernel<Prod, Comb, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
+      if (vec && allv)
+        red_cols_kernel<Prod, Comb, true, true><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
+      else if (vec)
+        red_cols_kernel<Prod, Comb, true, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
+      else
+        red_cols_kernel<Prod, Comb, false, false><<<grid, kBlock, 0, stream()>>>(A, prod, xblocks);
       if (chunks > 1) {  // the finalize reads the partials, and the inputs for a serial refold
         // chunks > 1 only when base_blocks < PLAST_COL_BLOCKS, so nout * Q lanes (at most
         // PLAST_COL_BLOCKS * 256 * Q) stay far inside one launch
