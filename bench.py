@@ -477,16 +477,19 @@ class C5(Workload):
 class C5Step(Workload):
     """Config 5's whole training step in one pass (softmax_cross_entropy_step_hip): logits
     [32768, 32000] ~ N(0, 2), labels U{0..31999}, dloss = 1/N (the mean's gradient); writes the
-    row statistics and loss, dlogits = dloss * (softmax - onehot) and dbias = sum_rows dlogits.
+    row statistics and loss, dlogits = dloss * (softmax - onehot), dbias = sum_rows dlogits and
+    the mean loss (the chain's MEAN, the scalar the reference's loss returns).
     Algorithmic bytes: the logits read once and dlogits written once (8 B/element), labels, dloss,
-    loss (4 B/row each), stats (8 B/row) and dbias (4 B/column); the workgroups' column-sum
-    partials (256 x 32000 x 4 B written and read) are workspace, not counted."""
+    loss (4 B/row each), stats (8 B/row), dbias (4 B/column), the loss read again for its mean
+    (4 B/row) and the mean (4 B); the workgroups' column-sum partials (256 x 32000 x 4 B written
+    and read) are workspace, not counted."""
     name = "config5_ce_step_one_pass"
 
     def __init__(self):
         self.N, self.C = 32768, 32000
         self.elems = self.N * self.C
-        self.bytes_per_call = 8 * self.elems + 4 * self.N * 3 + 8 * self.N + 4 * self.C
+        self.bytes_per_call = (8 * self.elems + 4 * self.N * 3 + 8 * self.N + 4 * self.C +
+                               4 * self.N + 4)
 
     def setup(self):
         N, Cn = self.N, self.C
@@ -497,10 +500,12 @@ class C5Step(Workload):
         self.loss = DeviceTensor((N,), zero=False)
         self.dx = DeviceTensor((N, Cn), zero=False)
         self.db = DeviceTensor((Cn,), zero=False)
+        self.mean = DeviceTensor((1,), zero=False)
 
     def step(self):
         lib().softmax_cross_entropy_step_hip(self.X.ptr, self.lab.ptr, self.g.ptr, self.st.ptr,
-                                             self.loss.ptr, self.dx.ptr, self.db.ptr, self.N, self.C)
+                                             self.loss.ptr, self.dx.ptr, self.db.ptr,
+                                             self.mean.ptr, self.N, self.C)
 
 
 class Optim(Workload):
@@ -578,6 +583,16 @@ class Pack(Workload):
             L.hip_tensor_pack_release(C.byref(p))
         else:
             L.plast_hip_tensor_to_host(C.byref(self.Av.t), self.host)
+
+    def plain_copy(self, steps: int, warmup: int) -> dict:
+        """The host link's ceiling for this row: a plain device-to-host copy of the same 256 MiB
+        from a contiguous device buffer into the same page-locked host buffer (one
+        hipMemcpyAsync on the library's stream, then a synchronize)."""
+        L = lib()
+        n = self.elems * 4
+        ms = timed(lambda: (L.arena_memcpy_d2h_hip(self.host, self.Ab.ptr, n),
+                            L.plast_hip_synchronize()), steps, warmup)
+        return {"ms": round(ms, 4), "GB_s": round(n / (ms * 1e-3) / 1e9, 2)}
 
     def free(self):
         if self.host:
@@ -777,6 +792,11 @@ def detail_workloads():
     }
 
 
+# --no-graphs: eager launches only (no graph capture or replay, no C call loop), for runs under a
+# tracer
+NO_GRAPHS = False
+
+
 def measure(w: Workload, steps: int, warmup: int) -> dict:
     w.setup()
     steps, warmup = max(steps, w.min_steps), max(warmup, w.min_steps // 10)
@@ -784,10 +804,17 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     gbs = w.bytes_per_call / (ms * 1e-3) / 1e9
     r = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
          "elems_per_s": round(w.elems / (ms * 1e-3), 1), "algorithmic_bytes": w.bytes_per_call}
+    if isinstance(w, Pack) and w.part == "host":
+        # the same bytes through a plain copy of a contiguous buffer: the link's ceiling
+        c = w.plain_copy(steps, warmup)
+        r["plain_d2h_copy"] = c
+        r["frac_of_plain_d2h_copy"] = round(c["ms"] / ms, 4)
     if isinstance(w, C1) and w.part not in ("big", "dagbig"):
         # latency-bound: microseconds per call as a Python caller and a C caller see them, and on
         # the device alone
         r["us_per_call"] = round(ms * 1e3, 2)
+        if NO_GRAPHS:
+            return r
         k = w.kernel_us()
         if k is not None:
             r["kernel_us_per_call"] = k
@@ -799,9 +826,10 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
 
 def check_step(w: "C5Step", rows=64) -> dict:
     """Bench-side parity of the headline: `rows` sampled rows against the oracle's cross-entropy
-    (row max bit-exact; log-sum-exp, loss and dlogits at 1e-5 relative), and the step's bias
+    (row max bit-exact; log-sum-exp, loss and dlogits at 1e-5 relative), the step's bias
     gradient against the library's own leading-axis sum of its dlogits (a separate kernel) at
-    1e-5 of sum |dlogits| per column."""
+    1e-5 of sum |dlogits| per column, and the mean loss against the float64 mean of the step's
+    per-row losses at 1e-5 of mean |loss|."""
     sys.path.insert(0, str(ROOT / "tests"))
     from hostlib import HostTensor, oracle_backward, oracle_forward
     N, Cn = w.N, w.C
@@ -835,8 +863,12 @@ def check_step(w: "C5Step", rows=64) -> dict:
     count = np.bincount(lab, minlength=Cn).astype(np.float64)
     scale = np.abs(db) + 2.0 * count * float(g.max()) + 1e-30
     worst["dbias"] = float(np.max(np.abs(db - rb) / scale))
+    # the mean loss against the float64 mean of the step's own per-row losses
+    mean, want = float(w.mean.numpy()[0]), float(lo.astype(np.float64).mean())
+    worst["mean_loss"] = abs(mean - want) / (float(np.abs(lo).astype(np.float64).mean()) + 1e-30)
     worst["ok"] = (worst["stats_max_bits"] == 0 and worst["lse"] <= 1e-5 and worst["loss"] <= 1e-5
-                   and worst["dlogits"] <= 1e-5 and worst["dbias"] <= 1e-5)
+                   and worst["dlogits"] <= 1e-5 and worst["dbias"] <= 1e-5
+                   and worst["mean_loss"] <= 1e-5)
     return worst
 
 
@@ -895,10 +927,15 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default="", help="comma list of detail keys (default: all)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="eager launches only: skip the graph-replayed and C-loop timings and the "
+                         "graph workload (for runs under a kernel tracer)")
     ap.add_argument("--compare", default="",
                     help="comma list of library builds (plast_amd.build --out): time the --only "
                          "workloads with each in turn in this process and print their medians")
     a = ap.parse_args(argv)
+    global NO_GRAPHS
+    NO_GRAPHS = a.no_graphs
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no collective or multi-GPU path is "
               "built); run with --gpus 1", file=sys.stderr)
@@ -918,10 +955,7 @@ def main(argv=None) -> int:
     ms = timed(head.step, a.steps, a.warmup)
     gbs = head.bytes_per_call / (ms * 1e-3) / 1e9
     L.plast_hip_synchronize()
-    parity = check_step(head)
-    log(f"config5 step: {ms:.4f} ms/step, {gbs:.1f} GB/s, parity {parity}")
-    if not parity["ok"]:
-        raise SystemExit(f"bench.py: config 5 step differs from the oracle: {parity}")
+    log(f"config5 step: {ms:.4f} ms/step, {gbs:.1f} GB/s")
 
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
@@ -931,8 +965,13 @@ def main(argv=None) -> int:
         except Exception:
             traffic = None
 
-    cpu, cpu_detail = None, {}
+    cpu, cpu_detail, parity = None, {}, None
     if not a.no_cpu:
+        # the CPU leg: the oracle checks sampled rows of the timed step's outputs, then is timed
+        parity = check_step(head)
+        log(f"config5 step parity: {parity}")
+        if not parity["ok"]:
+            raise SystemExit(f"bench.py: config 5 step differs from the oracle: {parity}")
         cpu = cpu_config5(head.X, head.lab)
         cpu["cores"] = int(os.environ["OMP_NUM_THREADS"])
         log(f"cpu baseline (config 5): {cpu}")
@@ -949,6 +988,8 @@ def main(argv=None) -> int:
     detail = {}
     if not a.no_detail:
         keys = [k for k in a.only.split(",") if k] or [k for k in detail_workloads() if k != "c5step"]
+        if a.no_graphs:
+            keys = [k for k in keys if k != "c1g"]
         for k in keys:
             w = detail_workloads()[k]
             try:
@@ -968,7 +1009,8 @@ def main(argv=None) -> int:
                                                        "bias gradient sum"],
                 "speedup_of_one_pass": round(sum(three) / ms, 3)}
     head_detail = {"ms": round(ms, 4), "GB_s": round(gbs, 1), "parity": parity,
-                   "launches_per_step": 2, "kernels": ["ce_step_kernel", "ce_step_finalize"]}
+                   "launches_per_step": 3,
+                   "kernels": ["ce_step_kernel", "ce_step_finalize", "ce_loss_mean_kernel"]}
 
     line = {
         "metric": METRIC,

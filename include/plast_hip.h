@@ -207,11 +207,14 @@ void relu_grad_modulate_bias_grad_hip(const float *dout, const float *out_data, 
  * reference, which runs the op chain of src/api/loss.c:97-169, its backward and the bias's ADD
  * backward as separate passes (its ADD backward accumulates the bias gradient with omp atomics,
  * kernel_macros.h:292-297, in no fixed order either); for callers that train with a
- * cross-entropy loss. All pointers are device memory; returns after the work completes (or is
- * queued, in asynchronous mode). */
+ * cross-entropy loss. When mean_loss is not NULL, mean_loss[0] = the mean of loss over the rows:
+ * the chain's last node, MEAN (src/api/loss.c:161-163), the scalar the reference's loss returns
+ * (summed in a fixed order, within the sum tolerance of the reference's serial sum; an overflowing
+ * sum is summed again in row order). All pointers are device memory; returns after the work
+ * completes (or is queued, in asynchronous mode). */
 void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, const float *dloss,
-                                    float *stats, float *loss, float *dlogits, float *dbias, u64 N,
-                                    u64 C);
+                                    float *stats, float *loss, float *dlogits, float *dbias,
+                                    float *mean_loss, u64 N, u64 C);
 
 /* softmax_cross_entropy_step_hip without allocating: same arguments and results, with its
  * per-workgroup column sums in a fixed 32 MiB device array of the library (each GPU holds its own
@@ -224,7 +227,8 @@ void softmax_cross_entropy_step_hip(const float *logits, const i32 *labels, cons
  * (other streams, other threads) share the array and race. No counterpart in the reference. */
 void softmax_cross_entropy_step_noalloc_hip(const float *logits, const i32 *labels,
                                             const float *dloss, float *stats, float *loss,
-                                            float *dlogits, float *dbias, u64 N, u64 C);
+                                            float *dlogits, float *dbias, float *mean_loss, u64 N,
+                                            u64 C);
 
 /* ------------------------------------------------------------------ pack / host transfer ----- */
 

@@ -157,9 +157,6 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_CE_NT_STORE
 #define PLAST_CE_NT_STORE 1
 #endif
-#ifndef PLAST_ROW_BLOCKED
-#define PLAST_ROW_BLOCKED 0  // persistent row kernels: rows strided over the grid (0) or blocked (1)
-#endif
 // Persistent row kernels: workgroup numbers renumbered so that each XCD holds a contiguous range
 // (1) or dispatch order (0). Measured in one process: softmax forward 5947 against 5920 GB/s, the
 // one-pass step unchanged (5759 / 5760): neutral within the 1-1.3% that two copies of one build
@@ -174,10 +171,6 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 // counter, against 6.53 for the flat copy.
 #ifndef PLAST_ROW_DYNAMIC
 #define PLAST_ROW_DYNAMIC 1
-#endif
-// Persistent row kernels: a compiler barrier after each issue of row loads (1) or none (0).
-#ifndef PLAST_ROW_PIN
-#define PLAST_ROW_PIN 1
 #endif
 #ifndef PLAST_CE_STEP_NT_LOAD
 #define PLAST_CE_STEP_NT_LOAD 1  // the one-pass step's row loads: nontemporal (1) or ordinary (0)
@@ -210,12 +203,10 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #define PLAST_COPY_XCD 1
 #endif
 // XCD-contiguous workgroup numbering elsewhere, measured (4 alternating runs each): row and
-// leading-axis reductions lose 3-12% with it (off); the flat cross-entropy backward gains 2.8% when
-// accumulating (on); a single-tensor SGD launch gains with it, a launch over many tensors loses
-// (on for one-entry launches only); Adam/AdamW with 64-lane workgroups lose 3% with it (off).
-#ifndef PLAST_RED_XCD
-#define PLAST_RED_XCD 0
-#endif
+// leading-axis reductions lose 3-12% with it (not used there); the flat cross-entropy backward
+// gains 2.8% when accumulating (on); a single-tensor SGD launch gains with it, a launch over many
+// tensors loses (on for one-entry launches only); Adam/AdamW with 64-lane workgroups lose 3% with
+// it (off).
 #ifndef PLAST_CE_BWD_XCD
 #define PLAST_CE_BWD_XCD 1
 #endif
@@ -224,15 +215,6 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #endif
 #ifndef PLAST_OPT_UNROLL
 #define PLAST_OPT_UNROLL 1    // optimizer updates: float4 units per lane
-#endif
-#ifndef PLAST_CE_BWD_MODE
-#define PLAST_CE_BWD_MODE 1  // cross-entropy backward: 0 (row, chunk) grid, 1 flat, 2 one workgroup per row
-#endif
-// Softmax forward over rows of 2048..32768 floats: 1 = persistent 1024-lane workgroups (one per
-// CU) walking rows with the next row's loads in flight; 0 = one 256-lane workgroup per row.
-// Measured at [32768, 32000]: 5.86-5.89 TB/s against 5.33-5.39.
-#ifndef PLAST_SOFTMAX_FWD_STEP
-#define PLAST_SOFTMAX_FWD_STEP 1
 #endif
 // Softmax forward and backward variants measured at [32768, 32000] in one process (so on the same
 // box and in the same process state): the persistent forward with one barrier per row (per-wave
@@ -245,6 +227,12 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #define PLAST_SOFTMAX_BWD_NT 1
 #endif
 // Softmax backward, rows held in registers: lanes per row.
+// Softmax backward: dx float4 units per lane loaded together with y and dy, ahead of the row's
+// reduction (at least V: all of them). Measured in one process at [32768, 32000]: none 5946 GB/s,
+// 4 units 5538, 8 units 5690, all 16 6099 (1024 lanes with all 8: 6103).
+#ifndef PLAST_SOFTMAX_BWD_PRE
+#define PLAST_SOFTMAX_BWD_PRE 32
+#endif
 #ifndef PLAST_SOFTMAX_BWD_BLOCK
 #define PLAST_SOFTMAX_BWD_BLOCK 512
 #endif

@@ -357,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void red_rows_kernel(RedArgs<Prod::NIN> A, 
   constexpr int NIN = Prod::NIN;
   using Part = typename Comb::Part;
   const int lane = threadIdx.x & 63;
-  const uint32_t bx = PLAST_RED_XCD ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint32_t bx = blockIdx.x;
   const uint64_t task = uint64_t(bx) * (kBlock / 64) + (threadIdx.x >> 6);
   if (task >= A.rows * A.segs) return;  // whole wave exits together
   const uint32_t row = uint32_t(task / A.segs);
@@ -590,13 +590,7 @@ __global__ __launch_bounds__(kBlock) void red_cols_kernel(RedArgs<Prod::NIN> A, 
   __shared__ Fast sh[kBlock / 64][64 * W];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  uint32_t bx = blockIdx.x, chunk = blockIdx.y;
-  if constexpr (PLAST_RED_XCD != 0) {
-    // renumber the (x, chunk) grid in dispatch order (x fastest)
-    const uint32_t lin = xcd_block(chunk * gridDim.x + bx, gridDim.x * gridDim.y);
-    chunk = lin / gridDim.x;
-    bx = lin - chunk * gridDim.x;
-  }
+  const uint32_t bx = blockIdx.x, chunk = blockIdx.y;
   const uint32_t o = bx / xblocks;
   const uint64_t j = (uint64_t(bx - o * xblocks) * 64 + lane) * W;
   const bool active = j < A.inner;  // no early return: the workgroup meets at a barrier

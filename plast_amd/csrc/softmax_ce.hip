@@ -290,49 +290,9 @@ __global__ __launch_bounds__(64 * kCeFwdWaves) void ce_fwd_wave_kernel(const flo
   }
 }
 
-// Backward, float4 path: a workgroup owns kBwdUnroll float4 per lane of one row; all of a lane's
-// loads are issued before any arithmetic.
+// Backward, any alignment: the scalar kernel's chunk of a row is kBwdUnroll * 4 * kCeBlock
+// elements.
 constexpr int kBwdUnroll = PLAST_CE_BWD_UNROLL;
-
-template <bool OVERWRITE>
-__global__ __launch_bounds__(kCeBlock) void ce_bwd_vec_kernel(const float *__restrict__ x,
-                                                              const int32_t *__restrict__ lab,
-                                                              const float *__restrict__ stats,
-                                                              const float *__restrict__ dloss,
-                                                              float *dx, uint32_t C, uint32_t chunks) {
-  const uint64_t row = blockIdx.x / chunks;
-  const uint32_t chunk = blockIdx.x - uint32_t(row) * chunks;
-  const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
-  const int32_t y = lab[row];
-  const uint32_t C4 = C / 4;
-  const f4 *x4 = reinterpret_cast<const f4 *>(x + row * C);
-  f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
-  const uint32_t q0 = chunk * (kCeBlock * kBwdUnroll) + threadIdx.x;
-  f4 xv[kBwdUnroll], dv[kBwdUnroll];
-#pragma unroll
-  for (int u = 0; u < kBwdUnroll; ++u) {
-    const uint32_t q = q0 + uint32_t(u) * kCeBlock;
-    if (q < C4) {
-      xv[u] = __builtin_nontemporal_load(x4 + q);
-      if constexpr (!OVERWRITE) dv[u] = __builtin_nontemporal_load(d4 + q);
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kBwdUnroll; ++u) {
-    const uint32_t q = q0 + uint32_t(u) * kCeBlock;
-    if (q >= C4) continue;
-    f4 r;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float sm = exp_le0((xv[u][c] - m) - l);
-      const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
-      const float gv = g * (sm - oh);
-      if constexpr (OVERWRITE) r[c] = gv;
-      else r[c] = dv[u][c] + gv;
-    }
-    store_stream<PLAST_CE_NT_STORE>(r, d4 + q);
-  }
-}
 
 // Backward, float4 path over the flattened [N, C] gradient: one float4 per lane, its row found by
 // magic division; the per-row constants are cached vector loads shared by the wave.
@@ -364,47 +324,6 @@ __global__ __launch_bounds__(kCeFlatBlock) void ce_bwd_flat_kernel(const float *
     else r[c] = dv[c] + gv;
   }
   store_stream<PLAST_CE_NT_STORE>(r, reinterpret_cast<f4 *>(dx) + q);
-}
-
-// Backward, float4 path: one workgroup per row, kBwdUnroll float4 per lane in flight per step.
-template <bool OVERWRITE>
-__global__ __launch_bounds__(kCeBlock) void ce_bwd_row_kernel(const float *__restrict__ x,
-                                                              const int32_t *__restrict__ lab,
-                                                              const float *__restrict__ stats,
-                                                              const float *__restrict__ dloss,
-                                                              float *dx, uint32_t C) {
-  const uint64_t row = blockIdx.x;
-  const float m = stats[2 * row], l = stats[2 * row + 1], g = dloss[row];
-  const int32_t y = lab[row];
-  const uint32_t C4 = C / 4;
-  const f4 *x4 = reinterpret_cast<const f4 *>(x + row * C);
-  f4 *d4 = reinterpret_cast<f4 *>(dx + row * C);
-  for (uint32_t q0 = threadIdx.x; q0 < C4; q0 += kCeBlock * kBwdUnroll) {
-    f4 xv[kBwdUnroll], dv[kBwdUnroll];
-#pragma unroll
-    for (int u = 0; u < kBwdUnroll; ++u) {
-      const uint32_t q = q0 + uint32_t(u) * kCeBlock;
-      if (q < C4) {
-        xv[u] = __builtin_nontemporal_load(x4 + q);
-        if constexpr (!OVERWRITE) dv[u] = __builtin_nontemporal_load(d4 + q);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kBwdUnroll; ++u) {
-      const uint32_t q = q0 + uint32_t(u) * kCeBlock;
-      if (q >= C4) continue;
-      f4 r;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float sm = exp_le0((xv[u][c] - m) - l);
-        const float oh = int32_t(q * 4 + c) == y ? 1.0f : 0.0f;
-        const float gv = g * (sm - oh);
-        if constexpr (OVERWRITE) r[c] = gv;
-        else r[c] = dv[u][c] + gv;
-      }
-      store_stream<PLAST_CE_NT_STORE>(r, d4 + q);
-    }
-  }
 }
 
 // Backward, any alignment: one element per lane per step.
@@ -455,22 +374,13 @@ __device__ __forceinline__ uint32_t row_block() {
   else return blockIdx.x;
 }
 
-// The rows a persistent row kernel's workgroup walks: r, r + S, ... below rend. Strided
-// (PLAST_ROW_BLOCKED 0): rows b, b + G, ..., so the grid sweeps the tensor front to back;
-// blocked (1): a contiguous block of ceil(N / G) rows per workgroup.
+// The rows a persistent row kernel's workgroup walks under the static schedule: r, r + S, ...
+// below rend, that is rows b, b + G, ..., so the grid sweeps the tensor front to back.
 __device__ __forceinline__ void row_range(uint32_t N, uint32_t G, uint32_t &r, uint32_t &S,
                                           uint32_t &rend) {
-  const uint32_t b = row_block();
-  if constexpr (PLAST_ROW_BLOCKED) {
-    const uint32_t per = (N + G - 1) / G;
-    r = b * per;
-    rend = r + per < N ? r + per : N;
-    S = 1;
-  } else {
-    r = b;
-    rend = N;
-    S = G;
-  }
+  r = row_block();
+  rend = N;
+  S = G;
 }
 
 // Dynamic row order for the persistent row kernels. Workgroups take pairs of rows (2P, 2P + 1) in
@@ -521,7 +431,7 @@ __device__ __forceinline__ f4 load_row_unit(const f4 *p) {
 // wait for the current row), which shortens the registers' live ranges but leaves nothing in
 // flight while the current row is reduced. A compiler-only barrier: no instruction is emitted.
 __device__ __forceinline__ void pin_loads() {
-  if constexpr (PLAST_ROW_PIN) asm volatile("" ::: "memory");
+  asm volatile("" ::: "memory");
 }
 
 constexpr int kStepBlock = PLAST_CE_STEP_BLOCK;
@@ -825,6 +735,44 @@ __global__ __launch_bounds__(kCeBlock) void ce_step_finalize(const float *__rest
   dbias[c] = t;
 }
 
+// The reference chain's last node: MEAN over the rows' losses (loss.c:161-163; the full
+// reduction of reduce_ops.c:24-31 with POST_MEAN, acc / n). One 1024-lane workgroup: lane l sums
+// rows l, l + 1024, ... in order, the waves' sums combine in a fixed order; a sum that overflowed
+// (finite terms, not a NaN) is summed again serially in row order, as the reference's order
+// decides it. Then divided by N.
+constexpr int kMeanBlock = 1024;
+__global__ __launch_bounds__(kMeanBlock) void ce_loss_mean_kernel(const float *__restrict__ loss,
+                                                                  float *__restrict__ out,
+                                                                  uint32_t N) {
+  __shared__ float sh[kMeanBlock / 64];
+  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  constexpr uint32_t kU = 8;
+  float s = 0.0f;
+  for (uint32_t i0 = t; i0 < N; i0 += kMeanBlock * kU) {
+    float v[kU];
+#pragma unroll
+    for (uint32_t k = 0; k < kU; ++k) {
+      const uint32_t i = i0 + k * kMeanBlock;
+      v[k] = loss[i < N ? i : N - 1];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kU; ++k)
+      if (i0 + k * kMeanBlock < N) s += v[k];
+  }
+  s = wave_sum(s);
+  if (lane == 0) sh[wave] = s;
+  __syncthreads();
+  if (t != 0) return;
+  float p = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kMeanBlock / 64; ++w) p += sh[w];
+  if (!(fabsf(p) <= FLT_MAX) && p == p) {
+    p = 0.0f;
+    for (uint32_t i = 0; i < N; ++i) p = p + loss[i];
+  }
+  out[0] = p / float(N);
+}
+
 // Whether ce_step_kernel<V> may be launched with its dynamic LDS (raising its limit once: beyond
 // the default the kernel has to opt in).
 template <int V>
@@ -917,6 +865,11 @@ void ce_step_launch(int V, unsigned grid, float *part, const float *logits, cons
   const uint32_t c32 = uint32_t(C);
   ce_step_launch_v<1>(V, grid, part, logits, labels, dloss, stats, loss, dlogits, uint32_t(N), c32);
   if (dbias) ce_step_finalize<<<ceil_div(C, kFinCols), kCeBlock, 0, stream()>>>(part, dbias, c32, grid);
+}
+
+// mean_loss[0] = the mean of loss[0 .. N) (N = 0: 0 / 0, NaN, as the reference's mean of nothing).
+void loss_mean(const float *loss, float *mean_loss, uint64_t N) {
+  ce_loss_mean_kernel<<<1, kMeanBlock, 0, stream()>>>(loss, mean_loss, uint32_t(N));
 }
 
 bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
@@ -1236,13 +1189,17 @@ __global__ __launch_bounds__(BS) void softmax_bwd_reg_kernel(const float *__rest
   // Loads are unconditional (a lane past the row reads the row's last float4, masked where it is
   // used): the compiler waits for every outstanding load before the first use of a lane-masked
   // one.
-  f4 yv[V], gv[V];
+  // the first kPre units of dx (all of them by default) are loaded with y and dy, so that their
+  // latency overlaps the row's reduction
+  constexpr int kPre = PLAST_SOFTMAX_BWD_PRE < V ? PLAST_SOFTMAX_BWD_PRE : V;
+  f4 yv[V], gv[V], dv[kPre > 0 ? kPre : 1];
 #pragma unroll
   for (int u = 0; u < V; ++u) {
     const uint32_t q = threadIdx.x + uint32_t(u) * BS;
     const uint32_t qc = q < C4 ? q : C4 - 1;
     yv[u] = __builtin_nontemporal_load(y4 + qc);
     gv[u] = __builtin_nontemporal_load(g4 + qc);
+    if (u < kPre) dv[u] = PLAST_SOFTMAX_BWD_NT ? __builtin_nontemporal_load(d4 + qc) : d4[qc];
   }
   float t = 0.0f;
 #pragma unroll
@@ -1256,7 +1213,9 @@ __global__ __launch_bounds__(BS) void softmax_bwd_reg_kernel(const float *__rest
   for (int u = 0; u < V; ++u) {
     const uint32_t q = threadIdx.x + uint32_t(u) * BS;
     if (q >= C4) continue;
-    f4 d = PLAST_SOFTMAX_BWD_NT ? __builtin_nontemporal_load(d4 + q) : d4[q];
+    f4 d;
+    if (u < kPre) d = dv[u < kPre ? u : 0];
+    else d = PLAST_SOFTMAX_BWD_NT ? __builtin_nontemporal_load(d4 + q) : d4[q];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       d[c] = d[c] + (LOG ? gv[u][c] - expf(yv[u][c]) * t : yv[u][c] * (gv[u][c] - t));
@@ -1301,7 +1260,7 @@ void softmax_forward(const Tensor **inputs, Tensor *output, KernelParams params,
       if (uint64_t(C) <= uint64_t(kSoftmaxBlock) * 4 * v) V = v;
   // rows of 2048..32768 floats: the persistent form (rows at a time below 2^31)
   int SV = 0;
-  if (PLAST_SOFTMAX_FWD_STEP && V && C >= 2048 && N < (uint64_t(1) << 31))
+  if (V && C >= 2048 && N < (uint64_t(1) << 31))
     for (int v = 1; v <= 8 && !SV; v *= 2)
       if (uint64_t(C) <= uint64_t(kStepBlock) * 4 * v) SV = v;
   if (SV) {
@@ -1456,21 +1415,14 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
     const float *pg = static_cast<const float *>(output->grad->data) + r0;
     const unsigned grid = unsigned(uint64_t(chunks) * n);
     const uint64_t units = n * C4;
-    if (vec && PLAST_CE_BWD_MODE == 1) {
+    if (vec) {
       const MagicDiv dc4 = MagicDiv::make(uint32_t(C4));
       const unsigned g = unsigned(ceil_div(units, kCeFlatBlock));
       if (over)
         ce_bwd_flat_kernel<true><<<g, kCeFlatBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
       else
         ce_bwd_flat_kernel<false><<<g, kCeFlatBlock, 0, stream()>>>(px, pl, ps, pg, pd, dc4, uint32_t(units));
-    } else if (vec && PLAST_CE_BWD_MODE == 2) {
-      if (over) ce_bwd_row_kernel<true><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
-      else ce_bwd_row_kernel<false><<<unsigned(n), kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C);
-    } else if (vec && over)
-      ce_bwd_vec_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
-    else if (vec)
-      ce_bwd_vec_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
-    else if (over)
+    } else if (over)
       ce_bwd_scalar_kernel<true><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
     else
       ce_bwd_scalar_kernel<false><<<grid, kCeBlock, 0, stream()>>>(px, pl, ps, pg, pd, C, chunks);
@@ -1479,11 +1431,14 @@ void softmax_cross_entropy_hip_backward(Tensor **inputs, const Tensor *output, K
 }
 
 void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, const float *dloss,
-                                    float *stats, float *loss, float *dlogits, float *dbias, u64 N,
-                                    u64 C) {
+                                    float *stats, float *loss, float *dlogits, float *dbias,
+                                    float *mean_loss, u64 N, u64 C) {
   const char *where = "softmax_cross_entropy_step_hip";
   if (!ensure_init()) return;
-  if (N == 0) return;
+  if (N == 0) {
+    if (mean_loss) loss_mean(loss, mean_loss, 0);
+    return;
+  }
   const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
   if (V < 0) return;
   if (V == 0) {
@@ -1512,6 +1467,10 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
     Tensor *bin[3] = {&tx, &tl, &ts};
     softmax_cross_entropy_hip_backward(bin, &to, KernelParams{0, 1, 0.0f});
     if (dbias) bias_grad_reduce_hip(dlogits, dbias, N * C, C);
+    if (mean_loss) {
+      loss_mean(loss, mean_loss, N);
+      finish(where);
+    }
     return;
   }
   const uint64_t grid = ce_step_grid(N, C);
@@ -1519,15 +1478,20 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
   if (!part) return;
   ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
+  if (mean_loss) loss_mean(loss, mean_loss, N);
   finish(where);
 }
 
 void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *labels,
                                             const float *dloss, float *stats, float *loss,
-                                            float *dlogits, float *dbias, u64 N, u64 C) {
+                                            float *dlogits, float *dbias, float *mean_loss, u64 N,
+                                            u64 C) {
   const char *where = "softmax_cross_entropy_step_noalloc_hip";
   if (!ensure_init()) return;
-  if (N == 0) return;
+  if (N == 0) {
+    if (mean_loss) loss_mean(loss, mean_loss, 0);
+    return;
+  }
   const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
   if (V < 0) return;
   if (V == 0) {
@@ -1540,6 +1504,7 @@ void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *
   if (!part) return;
   const uint64_t grid = ce_step_grid(N, C);
   ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
+  if (mean_loss) loss_mean(loss, mean_loss, N);
   finish(where);
 }
 

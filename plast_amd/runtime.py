@@ -87,8 +87,8 @@ class Library:
             "launch_relu_grad_modulate_hip": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
                                                C.c_float, C.c_int, C.c_int], None),
             "bias_grad_reduce_hip": ([C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64], None),
-            "softmax_cross_entropy_step_hip": ([C.c_void_p] * 7 + [C.c_uint64, C.c_uint64], None),
-            "softmax_cross_entropy_step_noalloc_hip": ([C.c_void_p] * 7 + [C.c_uint64, C.c_uint64],
+            "softmax_cross_entropy_step_hip": ([C.c_void_p] * 8 + [C.c_uint64, C.c_uint64], None),
+            "softmax_cross_entropy_step_noalloc_hip": ([C.c_void_p] * 8 + [C.c_uint64, C.c_uint64],
                                                        None),
             "relu_grad_modulate_bias_grad_hip": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                   C.c_uint64, C.c_uint64, C.c_float], None),

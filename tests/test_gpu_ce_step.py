@@ -20,6 +20,7 @@ import pytest
 
 from cases import assert_bits, assert_close_sum
 from hostlib import HostTensor, oracle_backward, oracle_forward
+from plast_amd import abi
 from plast_amd.abi import KernelParams
 
 pytestmark = pytest.mark.gpu
@@ -39,18 +40,43 @@ def deterministic(on=True):
         L.plast_hip_set_deterministic(old)
 
 
-def _step(rt, X, lab, g, with_bias=True):
+def _step(rt, X, lab, g, with_bias=True, want_mean=False):
     N, Cn = X.shape
     st = rt.DeviceTensor((N, 2), zero=False)
     loss = rt.DeviceTensor((N,), zero=False)
     dx = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 3, 5.0, 6.0)  # overwritten
     db = rt.DeviceTensor((Cn,), zero=False).fill_("uniform", 4, 5.0, 6.0) if with_bias else None
+    mean = rt.DeviceTensor((1,), zero=False).fill_("uniform", 5, 5.0, 6.0) if want_mean else None
     G = rt.DeviceTensor.from_numpy(g)
     L = rt.lib()
     L.softmax_cross_entropy_step_hip(X.ptr, lab.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr,
-                                     db.ptr if db is not None else None, N, Cn)
+                                     db.ptr if db is not None else None,
+                                     mean.ptr if mean is not None else None, N, Cn)
     L.check("ce step")
-    return st.numpy(), loss.numpy(), dx.numpy(), db.numpy() if db is not None else None
+    out = (st.numpy(), loss.numpy(), dx.numpy(), db.numpy() if db is not None else None)
+    return out + (float(mean.numpy()[0]),) if want_mean else out
+
+
+def _check_mean(mean, loss, wloss, wlse):
+    """The step's MEAN output against the oracle's mean (the reference's serial float sum, then
+    / N) of the step's own per-row losses at 1e-5 of sum |loss| / N, and of the oracle's losses
+    with the per-row loss bar added."""
+    N = loss.shape[0]
+    out = HostTensor(np.zeros(1, np.float32))
+    oracle_forward("mean", [HostTensor(loss.copy())], out, KernelParams(abi.DIM_ALL, 0, 0.0))
+    own = float(out.numpy()[0])
+    oracle_forward("mean", [HostTensor(wloss.copy())], out, KernelParams(abi.DIM_ALL, 0, 0.0))
+    ref = float(out.numpy()[0])
+    if np.isnan(ref):
+        assert np.isnan(mean) and np.isnan(own), f"mean {mean}, want NaN"
+        return
+    if np.isinf(own) or np.isinf(ref):
+        assert mean == own == ref, f"mean {mean}, its losses' mean {own}, the oracle's {ref}"
+        return
+    a = np.abs(loss.astype(np.float64)).sum() / N
+    assert abs(mean - own) <= 1e-5 * a + 1e-30, f"mean {mean} vs its losses' mean {own}"
+    b = (np.abs(wloss.astype(np.float64)) + np.abs(wlse.astype(np.float64)) + 1e-6).sum() / N
+    assert abs(mean - ref) <= 1e-5 * (a + b), f"mean {mean} vs the oracle's {ref}"
 
 
 def _oracle(x, lab, g):
@@ -93,11 +119,12 @@ def test_step_matches_oracle(N, Cn, special):
     g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)
     g[-1] = 0.5                    # the upstream gradient is per row
     X, Lb = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab)
-    st, loss, dx, db = _step(rt, X, Lb, g)
+    st, loss, dx, db, mean = _step(rt, X, Lb, g, want_mean=True)
     wst, wloss, wdx = _oracle(x, lab, g)
     assert_bits(st[:, 0], wst[:, 0], "row max")
     assert_close_sum(st[:, 1], wst[:, 1], np.abs(wst[:, 1]) + 1e-6, 1e-5, "row log-sum-exp")
     assert_close_sum(loss, wloss, np.abs(wloss) + np.abs(wst[:, 1]) + 1e-6, 1e-5, "row loss")
+    _check_mean(mean, loss, wloss, wst[:, 1])
     finite = np.isfinite(wdx).all(1)
     assert_close_sum(dx[finite], wdx[finite], np.abs(wdx[finite]) + 1e-2 / N, 1e-5, "dlogits")
     assert_bits(np.isnan(dx), np.isnan(wdx), "NaN positions of dlogits")
@@ -239,12 +266,13 @@ def test_step_many_rows_per_workgroup_matches_oracle(N, Cn, specials):
     g[GRID + 44 if GRID + 44 < N else 0] = 0.0
     g[2 * GRID + 5 if 2 * GRID + 5 < N else 1] = np.float32(-1.0 / N)
     X, Lb = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab)
-    st, loss, dx, db = _step(rt, X, Lb, g)
+    st, loss, dx, db, mean = _step(rt, X, Lb, g, want_mean=True)
     wst, wloss, wdx = _oracle(x, lab, g)
     assert_bits(st[:, 0], wst[:, 0], "row max")
     assert_close_sum(st[:, 1], wst[:, 1], np.abs(wst[:, 1]) + 1e-6, 1e-5, "row log-sum-exp")
     assert_close_sum(loss, wloss, np.abs(wloss) + np.abs(wst[:, 1]) + 1e-6, 1e-5, "row loss")
     assert_bits(np.isnan(loss), np.isnan(wloss), "NaN rows of the loss")
+    _check_mean(mean, loss, wloss, wst[:, 1])
     finite = np.isfinite(wdx).all(1)
     scale = np.abs(wdx[finite]) + np.abs(g[finite, None]) * 1e-2
     assert_close_sum(dx[finite], wdx[finite], scale, 1e-5, "dlogits")

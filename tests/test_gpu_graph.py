@@ -227,7 +227,7 @@ def test_workspace_outgrown_while_a_graph_lives():
             st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
             dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
             L.softmax_cross_entropy_step_hip(logits.ptr, labels.ptr, dloss.ptr, st.ptr, loss.ptr,
-                                             dx.ptr, db.ptr, N, Cn)
+                                             dx.ptr, db.ptr, None, N, Cn)
             L.check("ce step")
             assert L.plast_hip_workspace_retired() == retired0 + 2
         for rep in range(3):

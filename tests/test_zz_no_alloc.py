@@ -1,6 +1,6 @@
 """The allocation-free cross-entropy step (softmax_cross_entropy_step_noalloc_hip) against the
-allocating one (softmax_cross_entropy_step_hip) through the C-ABI: stats, loss, dlogits and the
-bias gradient bit for bit in deterministic mode (both run the same kernels over the same grid, one
+allocating one (softmax_cross_entropy_step_hip) through the C-ABI: stats, loss, dlogits, the mean
+loss and the bias gradient bit for bit in deterministic mode (both run the same kernels over the same grid, one
 rule shared by the two entry points; by default the bias gradient's split over workgroups follows
 the run's timing, so there it is held to the sum bar), on calls in a row whose second input is smaller than the first (the device array
 keeps the previous call's contents), with no workspace growth, recorded into a graph and replayed,
@@ -41,17 +41,22 @@ def _inputs(rt, N, Cn, seed, special=False):
             rt.DeviceTensor.from_numpy(g))
 
 
+NAMES = ("stats", "loss", "dlogits", "mean loss", "dbias")
+
+
 def _run(rt, entry, X, Lb, G, with_bias=True):
     N, Cn = X.shape
     st = rt.DeviceTensor((N, 2), zero=False).fill_("uniform", 1, 5.0, 6.0)
     loss = rt.DeviceTensor((N,), zero=False).fill_("uniform", 2, 5.0, 6.0)
     dx = rt.DeviceTensor((N, Cn), zero=False).fill_("uniform", 3, 5.0, 6.0)
+    mean = rt.DeviceTensor((1,), zero=False).fill_("uniform", 5, 5.0, 6.0)
     db = rt.DeviceTensor((Cn,), zero=False).fill_("uniform", 4, 5.0, 6.0) if with_bias else None
     L = rt.lib()
     getattr(L, entry)(X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr,
-                      db.ptr if db is not None else None, N, Cn)
+                      db.ptr if db is not None else None, mean.ptr, N, Cn)
     L.check(entry)
-    return [st.numpy(), loss.numpy(), dx.numpy()] + ([db.numpy()] if with_bias else [])
+    return ([st.numpy(), loss.numpy(), dx.numpy(), mean.numpy()] +
+            ([db.numpy()] if with_bias else []))
 
 
 def _same(rt, N, Cn, seed, special=False, with_bias=True):
@@ -61,14 +66,15 @@ def _same(rt, N, Cn, seed, special=False, with_bias=True):
     with deterministic(L):
         got = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
         want = _run(rt, "softmax_cross_entropy_step_hip", X, Lb, G, with_bias)
-    for name, a, b in zip(("stats", "loss", "dlogits", "dbias"), got, want):
+    for name, a, b in zip(NAMES, got, want):
         assert_bits(a, b, f"{N}x{Cn} {name}")
-    # the default (dynamic) order: per-row outputs the same bits, the bias gradient to the sum bar
+    # the default (dynamic) order: per-row outputs (and their mean, summed in a fixed order) the
+    # same bits, the bias gradient to the sum bar
     dyn = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G, with_bias)
-    for name, a, b in zip(("stats", "loss", "dlogits"), dyn, want):
+    for name, a, b in zip(NAMES[:4], dyn, want):
         assert_bits(a, b, f"{N}x{Cn} {name}, dynamic order")
     if with_bias:
-        assert_close_sum(dyn[3], want[3], np.abs(want[2]).astype(np.float64).sum(0) + 1e-12,
+        assert_close_sum(dyn[4], want[4], np.abs(want[2]).astype(np.float64).sum(0) + 1e-12,
                          1e-5, f"{N}x{Cn} dbias, dynamic order")
 
 
@@ -86,7 +92,7 @@ def test_no_workspace_is_touched():
         a = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
         b = _run(rt, "softmax_cross_entropy_step_noalloc_hip", X, Lb, G)
     assert [L.plast_hip_workspace_bytes(s) for s in range(3)] == before
-    for name, u, v in zip(("stats", "loss", "dlogits", "dbias"), a, b):
+    for name, u, v in zip(NAMES, a, b):
         assert_bits(u, v, f"repeat {name}")
 
 
@@ -101,15 +107,17 @@ def test_captured_no_alloc_step_replays():
     X, Lb, G = _inputs(rt, N, Cn, 12)
     st, loss = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
     dx, db = rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False)
-    args = (X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr, db.ptr, N, Cn)
+    mean = rt.DeviceTensor((1,), zero=False)
+    args = (X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr, db.ptr, mean.ptr, N, Cn)
+    outs = (st, loss, dx, mean, db)
     with deterministic(L):
-        _captured_replays(L, args, X, st, loss, dx, db, exact=True)
+        _captured_replays(L, args, X, outs, exact=True)
     # the default order: the counter its workgroups take rows from is returned to zero by every
     # launch, so replays of a captured launch cover every row too
-    _captured_replays(L, args, X, st, loss, dx, db, exact=False)
+    _captured_replays(L, args, X, outs, exact=False)
 
 
-def _captured_replays(L, args, X, st, loss, dx, db, exact):
+def _captured_replays(L, args, X, outs, exact):
     L.softmax_cross_entropy_step_noalloc_hip(*args)
     L.check("eager no-alloc")
     assert L.plast_hip_capture_begin() == 0
@@ -123,11 +131,11 @@ def _captured_replays(L, args, X, st, loss, dx, db, exact):
         for rep in range(3):
             X.fill_("normal", 100 + rep, 0.0, 2.0)
             assert L.plast_hip_graph_launch(graph) == 0
-            got = [t.numpy() for t in (st, loss, dx, db)]
+            got = [t.numpy() for t in outs]
             L.softmax_cross_entropy_step_noalloc_hip(*args)
             L.check("eager no-alloc")
-            now = [t.numpy() for t in (st, loss, dx, db)]
-            for name, u, v in zip(("stats", "loss", "dlogits", "dbias"), got, now):
+            now = [t.numpy() for t in outs]
+            for name, u, v in zip(NAMES, got, now):
                 if exact or name != "dbias":
                     assert_bits(u, v, f"replay {rep} {name}")
                 else:
@@ -159,6 +167,6 @@ def test_rows_beyond_the_one_pass_kernel_are_rejected():
         st, loss = rt.DeviceTensor((N, 2)), rt.DeviceTensor((N,))
         dx = rt.DeviceTensor((N, Cn))
         L.softmax_cross_entropy_step_noalloc_hip(X.ptr, Lb.ptr, G.ptr, st.ptr, loss.ptr, dx.ptr,
-                                                 None, N, Cn)
+                                                 None, None, N, Cn)
         with pytest.raises(rt.PlastHipError, match="not one-pass rows"):
             L.check("noalloc")
