@@ -711,12 +711,14 @@ def cpu_config5(X, lab, budget_s=12.0, rows=256):
 
     med, reps, spent = _repeat(one, budget_s)
     per_row = med / rows
-    bytes_per_row = 8 * Cn + 20
+    bytes_per_row = 8 * Cn + 24  # the step's bytes per row, its mean loss's read included
     return {"value": round(bytes_per_row / per_row / 1e9, 3), "unit": "GB/s", "kind": kind,
             "ms_full_step": round(per_row * N * 1e3, 1), "rows_per_s": round(1 / per_row, 1),
             "sample": f"{reps} chunks of {rows} rows x {Cn} of the same logits in {spent:.1f} s, "
                       f"median; GB/s counts the one-pass step's algorithmic bytes per row "
-                      f"({bytes_per_row} B); ms_full_step extrapolates to {N} rows"}
+                      f"({bytes_per_row} B); ms_full_step extrapolates to {N} rows; the "
+                      f"reference's CPU sources built by oracle/Makefile with -O3 -mavx2 -fopenmp "
+                      f"-ffp-contract=off (its own Makefile:7 has -O3 -march=native -fopenmp)"}
 
 
 def cpu_config1(budget_s=3.0):
