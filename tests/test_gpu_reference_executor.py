@@ -170,6 +170,27 @@ def test_config1_training_step_fused_through_the_reference_executor(
         assert_close_sum(db.reshape(-1), hb.grad.numpy().reshape(-1), scale, 1e-5, "db")
 
 
+def _random_case(seed):
+    rng = np.random.RandomState(seed)
+    C = int(rng.choice([1, 3, 4, 7, 64, 129, 256, 700]))
+    if rng.rand() < 0.3:
+        shape = (int(rng.randint(1, 9)), int(rng.randint(1, 200)), C)
+    else:
+        shape = (int(rng.choice([1, 2, 5, 31, 257, 1024, 3001])), C)
+    gx, gb = [(True, True), (True, False), (False, True)][rng.randint(3)]
+    return (f"random{seed}", shape, float(rng.choice([0.0, 0.01, 0.3])), gx, gb,
+            bool(rng.rand() < 0.5), bool(rng.rand() < 0.5), bool(rng.rand() < 0.5),
+            bool(rng.rand() < 0.5))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_fused_step_random_shapes(seed):
+    """Seeded random shapes (ranks 2 and 3, one row to 3001, one column to 700, float4 and
+    scalar forms), slopes, operand orders, bias forms and gradients wanted, through the same
+    check as the listed cases."""
+    test_config1_training_step_fused_through_the_reference_executor(*_random_case(seed))
+
+
 def test_config2_chain_as_a_training_graph():
     from plast_amd import runtime as rt
     print("reference executor: config 2 chain, forward and backward", flush=True)
