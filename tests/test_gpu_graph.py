@@ -2,9 +2,10 @@
 training step (the fused relu(X + b) chain, then grad_b = Σ_rows grad_Y through the split
 leading-axis reduction and its finalize) captured once and replayed several times, with fresh
 inputs uploaded eagerly between replays, each replay checked bit for bit against the same step
-run eagerly; plus a flat fused chain (2^20 elements, the tape interpreter), softmax with its backward and the one-pass
-epilogue captured and replayed, and the error paths (nested capture, a launch inside a capture,
-ending a capture that is not open)."""
+run eagerly; the same step as the DAG runs it with the fused leaky_relu(x + bias) node and its
+backward; plus a flat fused chain (2^20 elements, the tape interpreter), softmax with its backward
+and the one-pass epilogue captured and replayed, and the error paths (nested capture, a launch
+inside a capture, ending a capture that is not open)."""
 from __future__ import annotations
 
 import ctypes as C
@@ -62,6 +63,59 @@ def test_config1_step_replays_match_eager():
             step()                           # the same step, eagerly, on the same inputs
             assert_bits(y_g, Y.numpy(), f"replay {rep}: relu(X + b)")
             assert_bits(gb_g, gb.numpy(), f"replay {rep}: grad_b")
+    finally:
+        L.plast_hip_graph_destroy(graph)
+
+
+@pytest.mark.parametrize("shape", [(1024, 256), (4096, 1024)], ids=["config1", "4096x1024"])
+def test_fused_dag_step_replays(shape):
+    """Config 1's training step as the DAG runs it, the ADD -> LEAKY_RELU pair fused with
+    gradients (forward writing Y; backward writing dX and adding grad_b's column sums, in the
+    one-launch small form at config 1's size and the chunked pass with its finalize at the
+    larger one), captured once and replayed with fresh inputs and cleared gradients, each replay
+    bit for bit the same step run eagerly."""
+    from plast_amd.abi import KernelParams
+    from plast_amd.graph import Graph
+    rt = _rt()
+    L = rt.lib()
+    print(f"graph: fused dag step {shape}", flush=True)
+    R, Cn = shape
+    X = rt.DeviceTensor(shape, requires_grad=True, zero=False)
+    B = rt.DeviceTensor((Cn,), requires_grad=True, zero=False)
+    S = rt.DeviceTensor(shape, requires_grad=True, zero=False)
+    Y = rt.DeviceTensor(shape, requires_grad=True, zero=False)
+    g = Graph()
+    g.node("add", [X, B], S)
+    g.node("leaky_relu", [S], Y, KernelParams(0, 0, 0.0))
+    assert g.build(Y, fuse=True) == 1 and g.op_types() == ["FUSED_ELEMENTWISE"]
+
+    def fresh(seed):
+        X.fill_("uniform", seed, -1.0, 1.0)
+        B.fill_("uniform", seed + 1, -1.0, 1.0)
+        Y.grad.fill_("uniform", seed + 2, -1.0, 1.0)
+        X.grad.fill_("uniform", seed + 3, 0.0, 0.0)
+        B.grad.fill_("uniform", seed + 4, 0.0, 0.0)
+
+    def step():
+        g.forward()
+        g.backward()
+
+    fresh(10)
+    step()                                   # sizes the workspaces outside the capture
+    assert L.plast_hip_capture_begin() == 0
+    step()
+    graph = L.plast_hip_capture_end()
+    L.check("capture")
+    assert graph
+    try:
+        for rep in range(3):
+            fresh(20 + 10 * rep)
+            assert L.plast_hip_graph_launch(graph) == 0
+            got = [t.numpy() for t in (Y, X.grad, B.grad)]
+            fresh(20 + 10 * rep)
+            step()
+            for name, a, t in zip(("Y", "dX", "grad_b"), got, (Y, X.grad, B.grad)):
+                assert_bits(a, t.numpy(), f"replay {rep}: {name}")
     finally:
         L.plast_hip_graph_destroy(graph)
 
