@@ -474,8 +474,8 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     float *__restrict__ stats, float *__restrict__ loss, float *__restrict__ dx,
     float *__restrict__ part, uint32_t N, uint32_t C, uint32_t simd_end) {
   constexpr int BS = kStepBlock, W = BS / 64;
-  // one area per reduction round of a row: a round's single barrier orders its writes after every
-  // read of the same area in the previous row (which precede the other round's barrier)
+  // one area per reduction of a row: a reduction's single barrier orders its writes after every
+  // read of the same area in the previous row (which precede the other reduction's barrier)
   __shared__ float red1[2 * W], red2[W], ex[W + 2];
   __shared__ uint32_t tk;  // the next pair, from lane 0 of wave 0 (dynamic order)
   extern __shared__ f4 colsum[];  // BS * V float4: the workgroup's column sums, then padding
@@ -535,7 +535,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     if (next && t == 0) tk = give;
     const uint32_t ti = lane_index();
     const uint32_t full = C4 / BS;  // units every lane holds inside the row
-    // round 1: the row's max and min (lanes past the row hold a copy of its last float4, which
+    // first reduction: the row's max and min (lanes past the row hold a copy of its last float4, which
     // changes neither)
     float m = ninf, mn = pinf;
 #pragma unroll
@@ -571,7 +571,7 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
       M = fmaxf(M, red1[w]);
       MN = fminf(MN, red1[W + w]);
     }
-    // round 2: e = exp(x - M) into v, and its sum. A NaN logit reaches the sum; an infinite one,
+    // second reduction: e = exp(x - M) into v, and its sum. A NaN logit reaches the sum; an infinite one,
     // or an x - M that overflows, sends the row to the exact path below, so every value used from
     // here on came from a finite argument and the unclamped exponential is exact enough.
     float sl = 0.0f;
@@ -995,7 +995,7 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
                                                                       float *__restrict__ y,
                                                                       uint32_t N, uint32_t C) {
   constexpr int BS = kStepBlock, W = BS / 64;
-  // one area per reduction round (see ce_step_kernel)
+  // one area per reduction of a row (see ce_step_kernel)
   __shared__ float red1[2 * W], red2[W], ex[2];
   __shared__ uint32_t tk;  // the next pair, from lane 0 of wave 0 (dynamic order)
   const uint32_t C4 = C / 4, t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -1025,7 +1025,7 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
     if (next && t == 0) tk = give;
     const uint32_t ti = lane_index();
     const uint32_t full = C4 / BS;
-    // round 1: the fast maximum and whether the row holds a NaN (lanes past the row hold a copy of
+    // first reduction: the fast maximum and whether the row holds a NaN (lanes past the row hold a copy of
     // its last float4, which changes neither)
     float m = ninf;
     bool nan = false;
@@ -1059,7 +1059,7 @@ __global__ __launch_bounds__(kStepBlock) void softmax_fwd_step_kernel(const floa
     } else {
       mx = M > -FLT_MAX ? M : -FLT_MAX;
     }
-    // round 2: e = exp(x - mx), kept in v (log-softmax keeps x - mx), and the row's sum. A row with
+    // second reduction: e = exp(x - mx), kept in v (log-softmax keeps x - mx), and the row's sum. A row with
     // a NaN is summed from memory with expf instead (rare; it keeps the registers of the fast
     // path free), each lane over the same elements in the same order as the fast path.
     const f4 *x4 = reinterpret_cast<const f4 *>(x + uint64_t(r) * C);
