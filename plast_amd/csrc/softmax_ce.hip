@@ -361,10 +361,9 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // bits (a non-finite S or M, a zero M, an overflowing shifted-normalised logit) are recomputed
 // exactly from memory. Each lane adds the dx of its columns into the workgroup's column sums in LDS
 // (a slot per lane and unit; a lane only ever touches its own slots, so no synchronisation is
-// needed) across the
-// workgroup's rows; at the end the workgroup writes them to part[b][C], and ce_step_finalize adds
-// the G rows of part in workgroup order. No atomics: the bias gradient is deterministic for a
-// given grid. Registers hold the two row sets only (the column sums there would spill at 1024
+// needed) across the workgroup's rows; at the end the workgroup writes them to part[b][C], and
+// ce_step_tail adds the G rows of part in workgroup order. No atomics: the bias gradient is fixed
+// by which rows each workgroup took (the static schedule of deterministic mode fixes that too). Registers hold the two row sets only (the column sums there would spill at 1024
 // lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
 // A persistent row kernel's workgroup number b, which picks its rows and its partial-sum row:
 // the dispatch index, or (PLAST_ROW_XCD) that index renumbered so that each XCD holds a
@@ -703,74 +702,93 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
   }
 }
 
+// The step's tail, one launch after the row kernel: with `mean`, workgroup 0 writes the mean of
+// the rows' losses; the next `nfin` workgroups (with `dbias`) sum the row kernel's column sums.
+//
 // dbias[c] = the sum over workgroups b = 0 .. G-1 of part[b][c], deterministically: a workgroup
 // takes 32 columns; its lane group q (of 8) sums the q-th eighth of the b range in order (32 lanes
 // read 32 adjacent columns, 128 B, per row), then lane c adds the 8 group sums in q order.
+//
+// The mean is the reference chain's last node: MEAN over the rows' losses (loss.c:161-163; the
+// full reduction of reduce_ops.c:24-31 with POST_MEAN, acc / n). Its order is that of 1024 virtual
+// lanes: virtual lane L sums rows L, L + 1024, ... in order, each virtual wave of 64 lanes combines
+// its sums in a butterfly, and the 16 wave sums are added in wave order; a sum that overflowed
+// (finite terms, not a NaN) is summed again serially in row order, as the reference's order
+// decides it. Then divided by N (N = 0: 0 / 0, NaN, as the reference's mean of nothing). Lane p of
+// the 256 holds virtual lanes p + 256k (k < 4), which fall in virtual wave p / 64 + 4k at the same
+// position, so its four butterflies are those of the virtual waves; each lane keeps 32 loads in
+// flight (8 rows of 1024 at a time), as many as four rounds over config 5's 32768 rows.
 constexpr int kFinCols = 32, kFinGroups = kCeBlock / kFinCols;
-__global__ __launch_bounds__(kCeBlock) void ce_step_finalize(const float *__restrict__ part,
-                                                             float *__restrict__ dbias, uint32_t C,
-                                                             uint32_t G) {
+// partial rows (column sums) and rows of 1024 losses (mean) loaded at a time; 16 or 32 and 16
+// measured no faster (the launch's duration is not its loads' latency)
+constexpr uint32_t kFinBatch = 8, kMeanRounds = 8;
+constexpr uint32_t kMeanVirt = 1024, kMeanHold = kMeanVirt / kCeBlock;
+static_assert(kMeanVirt % kCeBlock == 0, "the mean's virtual lanes split evenly over the workgroup");
+__global__ __launch_bounds__(kCeBlock) void ce_step_tail(const float *__restrict__ part,
+                                                         float *__restrict__ dbias, uint32_t C,
+                                                         uint32_t G, const float *__restrict__ loss,
+                                                         float *__restrict__ mean, uint32_t N) {
   __shared__ float sh[kFinGroups][kFinCols];
-  const uint32_t cl = threadIdx.x % kFinCols, q = threadIdx.x / kFinCols;
-  const uint32_t c = blockIdx.x * kFinCols + cl;
+  const uint32_t t = threadIdx.x;
+  if (mean && blockIdx.x == 0) {
+    const uint32_t lane = t & 63, wave = t >> 6;
+    float s[kMeanHold] = {};
+    for (uint32_t i0 = t; i0 < N; i0 += kMeanVirt * kMeanRounds) {
+      float v[kMeanRounds][kMeanHold];
+#pragma unroll
+      for (uint32_t m = 0; m < kMeanRounds; ++m)
+#pragma unroll
+        for (uint32_t k = 0; k < kMeanHold; ++k) {
+          const uint32_t i = i0 + m * kMeanVirt + k * kCeBlock;
+          v[m][k] = loss[i < N ? i : N - 1];
+        }
+#pragma unroll
+      for (uint32_t m = 0; m < kMeanRounds; ++m)
+#pragma unroll
+        for (uint32_t k = 0; k < kMeanHold; ++k)
+          if (i0 + m * kMeanVirt + k * kCeBlock < N) s[k] += v[m][k];
+    }
+    float *ws = &sh[0][0];  // the virtual waves' sums, in virtual wave order
+#pragma unroll
+    for (uint32_t k = 0; k < kMeanHold; ++k) {
+      const float w = wave_sum(s[k]);
+      if (lane == 0) ws[wave + k * (kCeBlock / 64)] = w;
+    }
+    __syncthreads();
+    if (t != 0) return;
+    float p = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < kMeanVirt / 64; ++w) p += ws[w];
+    if (!(fabsf(p) <= FLT_MAX) && p == p) {
+      p = 0.0f;
+      for (uint32_t i = 0; i < N; ++i) p = p + loss[i];
+    }
+    mean[0] = p / float(N);
+    return;
+  }
+  const uint32_t cl = t % kFinCols, q = t / kFinCols;
+  const uint32_t c = (blockIdx.x - (mean ? 1u : 0u)) * kFinCols + cl;
   const uint32_t per = (G + kFinGroups - 1) / kFinGroups;
   const uint32_t b0 = q * per, b1 = b0 + per < G ? b0 + per : G;
   float s = 0.0f;
   if (c < C) {
-    for (uint32_t b = b0; b < b1; b += 8) {
-      float v[8];
+    for (uint32_t b = b0; b < b1; b += kFinBatch) {
+      float v[kFinBatch];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = b + k < b1 ? part[uint64_t(b + k) * C + c] : 0.0f;
+      for (uint32_t k = 0; k < kFinBatch; ++k)
+        v[k] = b + k < b1 ? part[uint64_t(b + k) * C + c] : 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (uint32_t k = 0; k < kFinBatch; ++k)
         if (b + k < b1) s += v[k];
     }
   }
   sh[q][cl] = s;
   __syncthreads();
   if (q != 0 || c >= C) return;
-  float t = sh[0][cl];
+  float u = sh[0][cl];
 #pragma unroll
-  for (int g = 1; g < kFinGroups; ++g) t += sh[g][cl];
-  dbias[c] = t;
-}
-
-// The reference chain's last node: MEAN over the rows' losses (loss.c:161-163; the full
-// reduction of reduce_ops.c:24-31 with POST_MEAN, acc / n). One 1024-lane workgroup: lane l sums
-// rows l, l + 1024, ... in order, the waves' sums combine in a fixed order; a sum that overflowed
-// (finite terms, not a NaN) is summed again serially in row order, as the reference's order
-// decides it. Then divided by N.
-constexpr int kMeanBlock = 1024;
-__global__ __launch_bounds__(kMeanBlock) void ce_loss_mean_kernel(const float *__restrict__ loss,
-                                                                  float *__restrict__ out,
-                                                                  uint32_t N) {
-  __shared__ float sh[kMeanBlock / 64];
-  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  constexpr uint32_t kU = 8;
-  float s = 0.0f;
-  for (uint32_t i0 = t; i0 < N; i0 += kMeanBlock * kU) {
-    float v[kU];
-#pragma unroll
-    for (uint32_t k = 0; k < kU; ++k) {
-      const uint32_t i = i0 + k * kMeanBlock;
-      v[k] = loss[i < N ? i : N - 1];
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < kU; ++k)
-      if (i0 + k * kMeanBlock < N) s += v[k];
-  }
-  s = wave_sum(s);
-  if (lane == 0) sh[wave] = s;
-  __syncthreads();
-  if (t != 0) return;
-  float p = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kMeanBlock / 64; ++w) p += sh[w];
-  if (!(fabsf(p) <= FLT_MAX) && p == p) {
-    p = 0.0f;
-    for (uint32_t i = 0; i < N; ++i) p = p + loss[i];
-  }
-  out[0] = p / float(N);
+  for (int g = 1; g < kFinGroups; ++g) u += sh[g][cl];
+  dbias[c] = u;
 }
 
 // Whether ce_step_kernel<V> may be launched with its dynamic LDS (raising its limit once: beyond
@@ -857,19 +875,25 @@ uint64_t ce_step_grid(uint64_t N, uint64_t C) {
   return N < grid ? N : grid;
 }
 
-// The one-pass step over `grid` workgroups with their column sums in part[grid][C], then their sum
-// into dbias when it is wanted.
-void ce_step_launch(int V, unsigned grid, float *part, const float *logits, const int32_t *labels,
-                    const float *dloss, float *stats, float *loss, float *dlogits, float *dbias,
-                    uint64_t N, uint64_t C) {
-  const uint32_t c32 = uint32_t(C);
-  ce_step_launch_v<1>(V, grid, part, logits, labels, dloss, stats, loss, dlogits, uint32_t(N), c32);
-  if (dbias) ce_step_finalize<<<ceil_div(C, kFinCols), kCeBlock, 0, stream()>>>(part, dbias, c32, grid);
+// The one-pass step over `grid` workgroups with their column sums in part[grid][C], then the tail:
+// their sum into dbias and the loss's mean, as wanted.
+// The step's tail: dbias from the column sums part[G][C] when dbias is wanted, and the mean of
+// loss[0 .. N) when mean_loss is; one launch, or none when neither is wanted.
+void step_tail(const float *part, float *dbias, uint64_t C, unsigned G, const float *loss,
+               float *mean_loss, uint64_t N) {
+  const uint64_t nfin = dbias ? ceil_div(C, kFinCols) : 0;
+  const uint64_t blocks = nfin + (mean_loss ? 1 : 0);
+  if (blocks)
+    ce_step_tail<<<unsigned(blocks), kCeBlock, 0, stream()>>>(part, dbias, uint32_t(C), G, loss,
+                                                             mean_loss, uint32_t(N));
 }
 
-// mean_loss[0] = the mean of loss[0 .. N) (N = 0: 0 / 0, NaN, as the reference's mean of nothing).
-void loss_mean(const float *loss, float *mean_loss, uint64_t N) {
-  ce_loss_mean_kernel<<<1, kMeanBlock, 0, stream()>>>(loss, mean_loss, uint32_t(N));
+void ce_step_launch(int V, unsigned grid, float *part, const float *logits, const int32_t *labels,
+                    const float *dloss, float *stats, float *loss, float *dlogits, float *dbias,
+                    float *mean_loss, uint64_t N, uint64_t C) {
+  const uint32_t c32 = uint32_t(C);
+  ce_step_launch_v<1>(V, grid, part, logits, labels, dloss, stats, loss, dlogits, uint32_t(N), c32);
+  step_tail(part, dbias, C, grid, loss, mean_loss, N);
 }
 
 bool check_ce(const Tensor *x, const Tensor *lab, const Tensor *st, const char *where) {
@@ -1436,7 +1460,8 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   const char *where = "softmax_cross_entropy_step_hip";
   if (!ensure_init()) return;
   if (N == 0) {
-    if (mean_loss) loss_mean(loss, mean_loss, 0);
+    step_tail(nullptr, nullptr, 0, 0, loss, mean_loss, 0);
+    if (mean_loss) finish(where);
     return;
   }
   const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
@@ -1468,7 +1493,7 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
     softmax_cross_entropy_hip_backward(bin, &to, KernelParams{0, 1, 0.0f});
     if (dbias) bias_grad_reduce_hip(dlogits, dbias, N * C, C);
     if (mean_loss) {
-      loss_mean(loss, mean_loss, N);
+      step_tail(nullptr, nullptr, 0, 0, loss, mean_loss, N);
       finish(where);
     }
     return;
@@ -1477,8 +1502,8 @@ void softmax_cross_entropy_step_hip(const float *logits, const int32_t *labels, 
   // the workgroups' column sums (written even when no bias gradient is wanted; then unread)
   float *part = static_cast<float *>(workspace(sizeof(float) * grid * C));
   if (!part) return;
-  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
-  if (mean_loss) loss_mean(loss, mean_loss, N);
+  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias,
+                 mean_loss, N, C);
   finish(where);
 }
 
@@ -1489,7 +1514,8 @@ void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *
   const char *where = "softmax_cross_entropy_step_noalloc_hip";
   if (!ensure_init()) return;
   if (N == 0) {
-    if (mean_loss) loss_mean(loss, mean_loss, 0);
+    step_tail(nullptr, nullptr, 0, 0, loss, mean_loss, 0);
+    if (mean_loss) finish(where);
     return;
   }
   const int V = ce_step_form(logits, labels, dloss, stats, loss, dlogits, N, C, where);
@@ -1503,8 +1529,8 @@ void softmax_cross_entropy_step_noalloc_hip(const float *logits, const int32_t *
   float *part = noalloc_scratch(where);
   if (!part) return;
   const uint64_t grid = ce_step_grid(N, C);
-  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias, N, C);
-  if (mean_loss) loss_mean(loss, mean_loss, N);
+  ce_step_launch(V, unsigned(grid), part, logits, labels, dloss, stats, loss, dlogits, dbias,
+                 mean_loss, N, C);
   finish(where);
 }
 
