@@ -9,7 +9,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from cases import assert_bits, assert_close_sum, assert_sum_parity
+from cases import LSE_SCALE, assert_bits, assert_close_sum, assert_sum_parity
 from hostlib import HostTensor, fused_chain2, oracle_backward, oracle_forward
 
 pytestmark = pytest.mark.gpu
@@ -220,8 +220,8 @@ def test_config5_softmax_ce(N, Cn):
     oracle_forward("softmax_cross_entropy", [hx, hl, hs], ho)
     st, wst = stats.numpy(), hs.numpy()
     assert_bits(st[:, 0], wst[:, 0], "row max")
-    assert_close_sum(st[:, 1], wst[:, 1], np.abs(wst[:, 1]) + 1e-6, 1e-5, "row log-sum-exp")
-    assert_close_sum(loss.numpy(), ho.numpy(), np.abs(ho.numpy()) + np.abs(wst[:, 1]) + 1e-6,
+    assert_close_sum(st[:, 1], wst[:, 1], LSE_SCALE, 1e-5, "row log-sum-exp")
+    assert_close_sum(loss.numpy(), ho.numpy(), np.abs(ho.numpy()) + LSE_SCALE,
                      1e-5, "row loss")
     # backward with dloss = 1/N (the MEAN node's backward)
     g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)

@@ -12,7 +12,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from cases import assert_bits, assert_close_sum
+from cases import LSE_SCALE, assert_bits, assert_close_sum
 from hostlib import HostTensor, oracle_backward, oracle_forward
 
 pytestmark = pytest.mark.gpu
@@ -77,9 +77,9 @@ def test_ce_rows_beyond_one_launch(C_):
     # l = log(s) with s the row's sum of exp terms (s >= 1): the sum tolerance |ds| <= 1e-5 * s
     # bounds |dl| by 1e-5 absolute (with three classes s is often near 1 and l tiny, so a
     # tolerance relative to l itself would ask for more than the sum's)
-    assert_close_sum(st[:, 1], wst[:, 1], 1.0, 1e-5, "row log-sum-exp")
+    assert_close_sum(st[:, 1], wst[:, 1], LSE_SCALE, 1e-5, "row log-sum-exp")
     got, want = loss.numpy(), ho.numpy()
-    assert_close_sum(got, want, np.abs(want) + np.abs(wst[:, 1]) + 1.0, 1e-5, "row loss")
+    assert_close_sum(got, want, np.abs(want) + LSE_SCALE, 1e-5, "row loss")
     zero_rows = [ROWS_PER_LAUNCH - 1, ROWS_PER_LAUNCH, se - 1, se, N - 1]
     assert_bits(got[zero_rows], want[zero_rows], "signed zero losses at the boundaries")
     assert np.signbit(got[se]) and not np.signbit(got[se - 1])
