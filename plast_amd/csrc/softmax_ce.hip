@@ -614,6 +614,9 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
     if (!exact) {
       const float gs = g * (1.0f / S);
       const float inv = 1.0f / S;
+      // each unit's gradient stored as soon as it is formed (the stores go out first), then the
+      // column sums, whose LDS reads and writes then run back to back without a branch between
+      // them (+1.4% over adding each unit before its store, in one process)
 #pragma unroll
       for (int u = 0; u < V; ++u) {
         const uint32_t q = ti + uint32_t(u) * BS;
@@ -623,9 +626,14 @@ __global__ __launch_bounds__(kStepBlock) void ce_step_kernel(
           for (int c = 0; c < 4; ++c)
             if (c == int(y & 3)) o[c] = g * (v[u][c] * inv - 1.0f);
         }
-        colsum[q] = colsum[q] + o;  // lanes past the row add into padding slots
         if (uint32_t(u) < full || q < C4)
           store_stream<PLAST_CE_NT_STORE>(o, reinterpret_cast<f4 *>(dr + q * 16u));
+        v[u] = o;
+      }
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const uint32_t q = ti + uint32_t(u) * BS;
+        colsum[q] = colsum[q] + v[u];  // lanes past the row add into padding slots
       }
     } else {
       // the exact statistics: the gradient from memory, as the backward op computes it
