@@ -436,3 +436,37 @@ def assert_sum_parity(gpu, ref, truth, scale, rel=1e-5, what=""):
         i = np.argwhere(~ok)[0]
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} fail; first at {tuple(i)}: "
                              f"gpu {g[tuple(i)]!r} ref {r[tuple(i)]!r} exact {t[tuple(i)]!r}")
+
+
+def check_ce_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, dx_floor, chunk=256):
+    """Row statistics, loss and dlogits against the oracle, each at its bar (scale) or - where the
+    oracle's serial exp-sum has drifted further than that from the exact value - at least as close
+    to the fp64 value as the oracle is: l = log(sum exp(x - m)) about the bit-exact max m, the loss
+    l - (x_y - m), dlogits g * (exp(x - m - l) - onehot). Over a long row the serial fp32 sum's
+    own error reaches 1e-5 of S (about sqrt(C) roundings). dlogits' scale is |oracle| + dx_floor
+    (per row); rows the oracle makes non-finite are left to the callers' NaN checks."""
+    N, Cn = x.shape
+    assert_bits(st[:, 0], wst[:, 0], "row max")
+    m = wst[:, 0].astype(np.float64)
+    l64 = np.empty(N)
+    for r0 in range(0, N, chunk):
+        with np.errstate(invalid="ignore", over="ignore"):
+            e = np.exp(x[r0:r0 + chunk].astype(np.float64) - m[r0:r0 + chunk, None])
+            l64[r0:r0 + chunk] = np.log(e.sum(1))
+    assert_sum_parity(st[:, 1], wst[:, 1], l64, LSE_SCALE, 1e-5, "row log-sum-exp")
+    xy = x[np.arange(N), lab].astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        assert_sum_parity(loss, wloss, l64 - (xy - m), np.abs(wloss) + LSE_SCALE, 1e-5, "row loss")
+    finite = np.isfinite(wdx).all(1)
+    floor = np.broadcast_to(np.asarray(dx_floor, np.float64), (N,))
+    for r0 in range(0, N, chunk):
+        rows = np.arange(r0, min(N, r0 + chunk))
+        rows = rows[finite[rows]]
+        if not rows.size:
+            continue
+        with np.errstate(invalid="ignore", over="ignore"):
+            t = np.exp(x[rows].astype(np.float64) - m[rows, None] - l64[rows, None])
+            t[np.arange(rows.size), lab[rows]] -= 1.0
+            t *= g[rows, None].astype(np.float64)
+        assert_sum_parity(dx[rows], wdx[rows], t, np.abs(wdx[rows]) + floor[rows, None], 1e-5,
+                          f"dlogits, rows {rows[0]}..{rows[-1]}")

@@ -19,7 +19,7 @@ import contextlib
 import numpy as np
 import pytest
 
-from cases import LSE_SCALE, assert_bits, assert_close_sum, assert_sum_parity
+from cases import LSE_SCALE, assert_bits, assert_close_sum, check_ce_rows
 from hostlib import HostTensor, oracle_backward, oracle_forward
 from plast_amd import abi
 from plast_amd.abi import KernelParams
@@ -92,40 +92,6 @@ def _oracle(x, lab, g):
     return hs.numpy(), ho.numpy(), hx.grad.numpy()
 
 
-def _check_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, dx_floor, chunk=256):
-    """Row statistics, loss and dlogits against the oracle, each at its bar (scale) or - where the
-    oracle's serial exp-sum has drifted further than that from the exact value - at least as close
-    to the fp64 value as the oracle is: l = log(sum exp(x - m)) about the bit-exact max m, the loss
-    l - (x_y - m), dlogits g * (exp(x - m - l) - onehot). Over a long row the serial fp32 sum's
-    own error reaches 1e-5 of S (about sqrt(C) roundings). dlogits' scale is |oracle| + dx_floor
-    (per row); rows the oracle makes non-finite are left to the callers' NaN checks."""
-    N, Cn = x.shape
-    assert_bits(st[:, 0], wst[:, 0], "row max")
-    m = wst[:, 0].astype(np.float64)
-    l64 = np.empty(N)
-    for r0 in range(0, N, chunk):
-        with np.errstate(invalid="ignore", over="ignore"):
-            e = np.exp(x[r0:r0 + chunk].astype(np.float64) - m[r0:r0 + chunk, None])
-            l64[r0:r0 + chunk] = np.log(e.sum(1))
-    assert_sum_parity(st[:, 1], wst[:, 1], l64, LSE_SCALE, 1e-5, "row log-sum-exp")
-    xy = x[np.arange(N), lab].astype(np.float64)
-    with np.errstate(invalid="ignore"):
-        assert_sum_parity(loss, wloss, l64 - (xy - m), np.abs(wloss) + LSE_SCALE, 1e-5, "row loss")
-    finite = np.isfinite(wdx).all(1)
-    floor = np.broadcast_to(np.asarray(dx_floor, np.float64), (N,))
-    for r0 in range(0, N, chunk):
-        rows = np.arange(r0, min(N, r0 + chunk))
-        rows = rows[finite[rows]]
-        if not rows.size:
-            continue
-        with np.errstate(invalid="ignore", over="ignore"):
-            t = np.exp(x[rows].astype(np.float64) - m[rows, None] - l64[rows, None])
-            t[np.arange(rows.size), lab[rows]] -= 1.0
-            t *= g[rows, None].astype(np.float64)
-        assert_sum_parity(dx[rows], wdx[rows], t, np.abs(wdx[rows]) + floor[rows, None], 1e-5,
-                          f"dlogits, rows {rows[0]}..{rows[-1]}")
-
-
 def _special_rows(x):
     N = x.shape[0]
     if N >= 8:
@@ -156,7 +122,7 @@ def test_step_matches_oracle(N, Cn, special):
     X, Lb = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab)
     st, loss, dx, db, mean = _step(rt, X, Lb, g, want_mean=True)
     wst, wloss, wdx = _oracle(x, lab, g)
-    _check_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, 1e-2 / N)
+    check_ce_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, 1e-2 / N)
     _check_mean(mean, loss, wloss)
     assert_bits(np.isnan(dx), np.isnan(wdx), "NaN positions of dlogits")
     # the bias gradient against the column sums of the oracle's dlogits (float64)
@@ -301,7 +267,7 @@ def test_step_many_rows_per_workgroup_matches_oracle(N, Cn, specials):
     X, Lb = rt.DeviceTensor.from_numpy(x), rt.DeviceTensor.from_numpy(lab)
     st, loss, dx, db, mean = _step(rt, X, Lb, g, want_mean=True)
     wst, wloss, wdx = _oracle(x, lab, g)
-    _check_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, np.abs(g) * 1e-2)
+    check_ce_rows(x, lab, g, st, loss, dx, wst, wloss, wdx, np.abs(g) * 1e-2)
     assert_bits(np.isnan(loss), np.isnan(wloss), "NaN rows of the loss")
     _check_mean(mean, loss, wloss)
     assert_bits(np.isnan(dx), np.isnan(wdx), "NaN positions of dlogits")

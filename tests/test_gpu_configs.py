@@ -9,7 +9,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from cases import LSE_SCALE, assert_bits, assert_close_sum, assert_sum_parity
+from cases import assert_bits, assert_close_sum, assert_sum_parity, check_ce_rows
 from hostlib import HostTensor, fused_chain2, oracle_backward, oracle_forward
 
 pytestmark = pytest.mark.gpu
@@ -219,10 +219,6 @@ def test_config5_softmax_ce(N, Cn):
     hs, ho = _host(np.zeros((N, 2), np.float32)), _host(np.zeros(N, np.float32), grad=True)
     oracle_forward("softmax_cross_entropy", [hx, hl, hs], ho)
     st, wst = stats.numpy(), hs.numpy()
-    assert_bits(st[:, 0], wst[:, 0], "row max")
-    assert_close_sum(st[:, 1], wst[:, 1], LSE_SCALE, 1e-5, "row log-sum-exp")
-    assert_close_sum(loss.numpy(), ho.numpy(), np.abs(ho.numpy()) + LSE_SCALE,
-                     1e-5, "row loss")
     # backward with dloss = 1/N (the MEAN node's backward)
     g = np.full(N, np.float32(1.0) / np.float32(N), np.float32)
     rt.lib().arena_memcpy_h2d_hip(loss.grad.ptr, g.ctypes.data, g.nbytes)
@@ -230,8 +226,9 @@ def test_config5_softmax_ce(N, Cn):
     rt.backward("softmax_cross_entropy", [dx, dl, stats], loss)
     oracle_backward("softmax_cross_entropy", [hx, hl, hs], ho)
     gx, wx = dx.grad.numpy(), hx.grad.numpy()
-    finite = np.isfinite(wx).all(1)
-    assert_close_sum(gx[finite], wx[finite], np.abs(wx[finite]) + 1.0 / N * 1e-2, 1e-5, "dlogits")
+    # statistics, loss and dlogits against the oracle, or the fp64 value where its serial
+    # exp-sum drifts
+    check_ce_rows(x, lab, g, st, loss.numpy(), gx, wst, ho.numpy(), wx, 1e-2 / N)
     # overwrite mode gives the same values into a fresh buffer
     dx2 = rt.DeviceTensor.from_numpy(x, requires_grad=True)
     rt.backward("softmax_cross_entropy", [dx2, dl, stats], loss, KernelParams(0, 1, 0.0))
