@@ -126,6 +126,15 @@ constexpr int kBlock = 256;  // threads per workgroup for streaming kernels (4 w
 #ifndef PLAST_COL_SMALL_S4_3
 #define PLAST_COL_SMALL_S4_3 1
 #endif
+// rows each lane loads per batch in the small leading-axis sum (three operands and more: config 1's
+// fused backward step 10.6 -> 10.0 us on the device with 4, 10.1 with 2, against 8; one operand
+// keeps 8, with 2 its grad_b launch ran 9% slower)
+#ifndef PLAST_COL_SMALL_U
+#define PLAST_COL_SMALL_U 8
+#endif
+#ifndef PLAST_COL_SMALL_U3
+#define PLAST_COL_SMALL_U3 4
+#endif
 #ifndef PLAST_COL_SMALL3
 #define PLAST_COL_SMALL3 1
 #endif

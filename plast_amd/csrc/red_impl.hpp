@@ -560,6 +560,8 @@ template <class Prod>
 constexpr int kColMinRows = Prod::NIN >= 3 ? PLAST_COL_MIN_ROWS3 : 64;
 template <class Prod>
 constexpr int kColSmallS4 = Prod::NIN >= 3 ? PLAST_COL_SMALL_S4_3 : PLAST_COL_SMALL_S4;
+template <class Prod>
+constexpr int kColSmallU = Prod::NIN >= 3 ? PLAST_COL_SMALL_U3 : PLAST_COL_SMALL_U;
 
 // Fast summary of an order-sensitive fold (exact max/min): the plain extreme and a NaN flag.
 struct ExtFast {
@@ -725,7 +727,7 @@ template <class Prod, bool ALLV>
 __global__ __launch_bounds__(kBlock) void red_cols_small_kernel(RedArgs<Prod::NIN> A, Prod prod,
                                                                 uint32_t xblocks) {
   constexpr int NIN = Prod::NIN;
-  constexpr int S4 = kColSmallS4<Prod>, G = kBlock / S4, kU = 8;
+  constexpr int S4 = kColSmallS4<Prod>, G = kBlock / S4, kU = kColSmallU<Prod>;
   static_assert(64 % S4 == 0, "row groups split evenly over the waves");
   __shared__ f4 sh[kBlock / 64][S4];
   const uint32_t t = threadIdx.x, c4 = t % S4, g = t / S4, lane = t & 63, wv = t >> 6;
