@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c4r,...] [--no-cpu]
     python bench.py --only KEYS --compare LIB1.so,LIB2.so   (builds timed against each other)
+    python bench.py --placement adam|epilogue               (a kernel's arrays at set offsets)
 
 Prints ONE JSON line. `value` is config 5 (the largest single-GPU
 config): a whole softmax-cross-entropy training step over [32768, 32000] fp32 logits - the forward's
@@ -934,6 +935,56 @@ def compare_builds(a) -> int:
     return 0
 
 
+def placement_probe(kind: str) -> int:
+    """The relative placement of a kernel's arrays as the variable: Adam over 64M parameters (p,
+    g, m, v) or the one-pass epilogue over [16384, 4096] (dout, out, dc), with the arrays carved
+    from one allocation 2^26 floats plus 16 MiB of slack apart and array k shifted by k times a
+    skew (1 KiB to 4 MiB; for the epilogue also dc first, then out, then dout). Two passes in one
+    process; prints one JSON line of GB/s (algorithmic bytes / HIP-event time) per placement."""
+    L = lib()
+    L.plast_hip_set_sync(0)
+    n, pad = 1 << 26, 1 << 22
+    arrays = {"adam": 4, "epilogue": 3}[kind]
+    big = DeviceTensor((arrays * (n + pad),), zero=False).fill_("normal", 7, 0.0, 1.0)
+    keep = []
+    if kind == "adam":
+        def call(ptr):
+            g = abi.make_tensor(ptr[1], (n,))
+            prm = abi.make_tensor(ptr[0], (n,), requires_grad=True, grad=g)
+            m, v = abi.make_tensor(ptr[2], (n,)), abi.make_tensor(ptr[3], (n,))
+            marr, varr = (abi.TensorP * 1)(C.pointer(m)), (abi.TensorP * 1)(C.pointer(v))
+            opt = abi.Adam(1e-3, 0.9, 0.999, 1e-8, 0, None, None, None, None)
+            opt.m, opt.v = C.cast(marr, abi.TensorPP), C.cast(varr, abi.TensorPP)
+            parr = (abi.TensorP * 1)(C.pointer(prm))
+            keep[:] = [g, prm, m, v, marr, varr, opt, parr]
+            pp = C.cast(parr, abi.TensorPP)
+            return lambda: L.adam_step_hip(C.byref(opt), pp, 1)
+        bytes_per = 28
+    else:
+        db = DeviceTensor((4096,), zero=False)
+        keep.append(db)
+
+        def call(ptr):
+            return lambda: L.relu_grad_modulate_bias_grad_hip(ptr[0], ptr[1], ptr[2], db.ptr, n,
+                                                              4096, 0.01)
+        bytes_per = 12
+    cases = {"aligned": [0] * arrays}
+    for kb in (1, 2, 4, 8, 16, 64, 256, 1024, 4096):
+        cases[f"{kb}K skew"] = [k * kb * 256 for k in range(arrays)]
+    if kind == "epilogue":
+        cases["dc first"] = [2 * (n + pad), -(n + pad), -(n + pad)]
+    res = {name: [] for name in cases}
+    for _ in range(2):
+        for name, skews in cases.items():
+            ptr = [big.ptr + 4 * (k * (n + pad) + sk) for k, sk in enumerate(skews)]
+            ms = timed(call(ptr), 20, 5, warm_ms=30.0)
+            res[name].append(round(bytes_per * n / (ms * 1e-3) / 1e9, 1))
+            log(f"{kind} {name}: {res[name][-1]} GB/s")
+    big.free()
+    print(json.dumps({"placement": kind, "GB_s": res}), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -947,6 +998,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-graphs", action="store_true",
                     help="eager launches only: skip the graph-replayed and C-loop timings and the "
                          "graph workload (for runs under a kernel tracer)")
+    ap.add_argument("--placement", default="", choices=["", "adam", "epilogue"],
+                    help="time one kernel with its arrays at chosen relative offsets in one "
+                         "allocation (a placement probe) and print its JSON line")
     ap.add_argument("--compare", default="",
                     help="comma list of library builds (plast_amd.build --out): time the --only "
                          "workloads with each in turn in this process and print their medians")
@@ -957,6 +1011,8 @@ def main(argv=None) -> int:
         print("bench.py: this build measures one GPU only (no collective or multi-GPU path is "
               "built); run with --gpus 1", file=sys.stderr)
         return 2
+    if a.placement:
+        return placement_probe(a.placement)
     if a.compare:
         return compare_builds(a)
     cores = host_cores()
