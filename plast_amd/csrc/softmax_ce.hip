@@ -353,7 +353,8 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // ---- a whole cross-entropy training step in one pass: the forward's row statistics and loss,
 // the backward's dx = dloss * (softmax - onehot), and the bias gradient sum_rows dx, reading each
 // logit once and writing each gradient once. Persistent workgroups of kStepBlock lanes walk rows
-// b, b + G, b + 2G, ...; a row is held in registers (V float4 per lane; lanes past the row are
+// in pairs taken from a device counter (in deterministic mode, rows b, b + G, b + 2G, ...); a row
+// is held in registers (V float4 per lane; lanes past the row are
 // masked), and the next row's loads are issued into a second register set before the current row is
 // reduced, so memory keeps streaming through the row's two block reductions. Per row, with the
 // forward kernel's semantics (ce_fwd_wave_kernel): M = the block max, S = sum exp(x - M) in the
@@ -363,8 +364,9 @@ __global__ __launch_bounds__(kCeBlock) void ce_bwd_scalar_kernel(const float *__
 // (a slot per lane and unit; a lane only ever touches its own slots, so no synchronisation is
 // needed) across the workgroup's rows; at the end the workgroup writes them to part[b][C], and
 // ce_step_tail adds the G rows of part in workgroup order. No atomics: the bias gradient is fixed
-// by which rows each workgroup took (the static schedule of deterministic mode fixes that too). Registers hold the two row sets only (the column sums there would spill at 1024
-// lanes per workgroup, whose wave count caps a lane at 128 VGPRs).
+// by which rows each workgroup took (the static schedule of deterministic mode fixes that too).
+// Registers hold the two row sets only (the column sums there would spill at 1024 lanes per
+// workgroup, whose wave count caps a lane at 128 VGPRs).
 // A persistent row kernel's workgroup number b, which picks its rows and its partial-sum row:
 // the dispatch index, or (PLAST_ROW_XCD) that index renumbered so that each XCD holds a
 // contiguous range of b.
