@@ -204,6 +204,59 @@ def test_step_full_size_properties():
     assert abs(db.astype(np.float64).sum()) <= 1e-4
 
 
+def test_step_full_size_repeats():
+    """Config 5 at [32768, 32000], called repeatedly: in deterministic mode every output repeats
+    bit for bit; in the default order the per-row outputs (statistics, loss, each dlogits row's sum
+    and max taken by the library's fixed-order reductions) and the mean repeat bit for bit and equal
+    the deterministic ones, and the bias gradient stays within 1e-5 of the sum of its terms'
+    magnitudes of the deterministic one."""
+    from plast_amd import ops, runtime as rt
+    from plast_amd.abi import INT32
+    N, Cn = 32768, 32000
+    print("ce step full size, repeated calls", flush=True)
+    L = rt.lib()
+    X = rt.DeviceTensor((N, Cn), zero=False).fill_("normal", 42, 0.0, 2.0)
+    Lb = rt.DeviceTensor((N,), INT32, zero=False).fill_("randint", 45, 0, Cn)
+    G = rt.DeviceTensor((N,), zero=False).fill_("uniform", 7, 1.0 / N, 1.0 / N)
+    st, lo = rt.DeviceTensor((N, 2), zero=False), rt.DeviceTensor((N,), zero=False)
+    dx, db, mn = (rt.DeviceTensor((N, Cn), zero=False), rt.DeviceTensor((Cn,), zero=False),
+                  rt.DeviceTensor((1,), zero=False))
+
+    def call():
+        L.softmax_cross_entropy_step_hip(X.ptr, Lb.ptr, G.ptr, st.ptr, lo.ptr, dx.ptr, db.ptr,
+                                         mn.ptr, N, Cn)
+        L.check("softmax_cross_entropy_step_hip")
+        out = dict(st=st.numpy(), loss=lo.numpy(), mean=mn.numpy(),
+                   rsum=ops.reduce("sum", dx, dim=1).numpy(),
+                   rmax=ops.reduce("max", dx, dim=1).numpy(), db=db.numpy())
+        return {k: v.copy() for k, v in out.items()}
+
+    rows = ("st", "loss", "mean", "rsum", "rmax")
+    try:
+        with deterministic():
+            ref = call()
+            for i in range(8):
+                got = call()
+                for k in rows + ("db",):
+                    assert_bits(got[k], ref[k], f"deterministic call {i + 2}: {k}")
+        first = call()
+        for k in rows:
+            assert_bits(first[k], ref[k], f"default order: {k} against deterministic mode")
+        dxh = dx.numpy()
+        acol = np.zeros(Cn)
+        for r0 in range(0, N, 2048):
+            acol += np.abs(dxh[r0:r0 + 2048].astype(np.float64)).sum(0)
+        del dxh
+        for i in range(8):
+            got = call()
+            for k in rows:
+                assert_bits(got[k], first[k], f"default order, call {i + 2}: {k}")
+            assert_close_sum(got["db"], ref["db"], acol + 1e-12, 1e-5, f"default order, call {i + 2}: dbias")
+    finally:
+        for t in (X, Lb, G, st, lo, dx, db, mn):
+            t.free()
+
+
 # Rows outnumber the one-pass step's workgroups (one per CU, 256 on MI355X) several times over, and
 # the row count is not a multiple of the grid: each workgroup's loop runs many iterations,
 # alternates its two register sets, ends on either set (odd and even row counts per workgroup) and
