@@ -23,7 +23,11 @@ pytestmark = pytest.mark.gpu
 # (600, 2052), (600, 2048) and (300, 8192) give the persistent forward more rows than workgroups
 # (with special rows in later iterations), the first with a partial last float4 unit per lane
 SHAPES = [(4, 10), (33, 1000), (8, 32000), (2, 3, 257), (1, 1), (5, 4096), (6, 9), (600, 2052),
-          (600, 2048), (300, 8192)]
+          (600, 2048), (300, 8192),
+          # from a wider seeded sweep: 1200 rows of 32000 (four or five per workgroup, the late
+          # special rows in both register sets), rows of 5000 over three leading axes, and rows
+          # that are not whole float4 (1023) or one workgroup's width (1024)
+          (2, 600, 32000), (3, 100, 5000), (300, 1023), (2, 300, 1024)]
 
 
 def _put_specials(rows, r0):
