@@ -183,7 +183,7 @@ def _random_case(seed):
             bool(rng.rand() < 0.5))
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(64))
 def test_fused_step_random_shapes(seed):
     """Seeded random shapes (ranks 2 and 3, one row to 3001, one column to 700, float4 and
     scalar forms), slopes, operand orders, bias forms and gradients wanted, through the same
